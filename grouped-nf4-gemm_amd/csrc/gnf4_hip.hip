@@ -1,0 +1,795 @@
+// gnf4_hip.hip -- grouped 4-bit (NF4 / MXFP4) MoE expert GEMM for CDNA4 (gfx950).
+//
+// Computes, for tokens grouped by expert, out[t, :] = a[t, :] . dequant(W[e(t)])^T
+// (forward) and grad_a[t, :] = grad_out[t, :] . dequant(W[e(t)]) (dgrad), in one
+// launch for all active experts, from the packed [E, N, K/2] uint8 weights.
+//
+// Weight decode, shared by every kernel here (reference semantics:
+// kernel/nf4_grouped.py:910-929 and kernel/mxfp4_pack_ref.py:46-70):
+//   NF4   byte j of a row holds elements 2j (high nibble) and 2j+1 (low
+//         nibble); w = NF4[code] * absmax[n, k / 64] is formed in fp32 (one
+//         rounding) and rounded once to bf16 (RNE). The LUT lookup is a
+//         64 KiB LDS table indexed by the whole packed byte: entry (byte, lane)
+//         holds the fp32 pair (NF4[byte >> 4], NF4[byte & 15]) in a column
+//         private to lane % 32, so a wave's 64 lookups never share an LDS
+//         bank. One v_perm_b32 forms the byte address (byte << 8 | lane*8).
+//   MXFP4 byte j holds elements 2j (low nibble) and 2j+1 (high nibble);
+//         v_cvt_scalef32_pk_bf16_fp4 converts a nibble pair and multiplies by
+//         2^(e - 127) in one instruction. e2m1 x 2^s is exact in bf16.
+// The decoded bf16 weights feed v_mfma_f32_16x16x32_bf16 with fp32
+// accumulation and a single bf16 rounding of each output.
+//
+// MFMA 16x16x32 operand layout used throughout (lane l = 0..63):
+//   A: row l % 16, 8 consecutive k of slice (l / 16)
+//   B: col l % 16, 8 consecutive k of slice (l / 16)
+//   D: rows 4 * (l / 16) + i (i = 0..3), col l % 16
+// The k-slice assignment only has to agree between A and B.
+//
+// Kernels:
+//   k_decode_fwd   groups of <= 16 rows (decode). One wave streams a 16-row
+//                  weight tile straight from HBM through registers, 16 bytes
+//                  per lane per 128-element chunk, with a prefetch ring; the
+//                  group's <= 16 activation rows ride along as the MFMA A
+//                  operand. Persistent grid, units = (group, 16-row n-tile).
+//   k_gemm_fwd     large groups (prefill). BM x 128 output tiles over ragged
+//                  groups from a host tile table; per 64-wide k-step the
+//                  activation tile and the decoded weight tile are staged in
+//                  LDS (double buffered) and consumed by 4 waves.
+//   k_gemm_dgrad   grad_a = grad_out . W, contracting over N in fixed 64-wide
+//                  steps (two MFMAs, ascending n) so the output bits do not
+//                  depend on the output tiling. The weight tile is decoded
+//                  from the same [E, N, K/2] layout and written to LDS
+//                  transposed (k-major) for the MFMA B operand.
+//
+// Everything is stream-ordered on the caller's stream. No allocation, no
+// host synchronisation. Return codes: 0 ok, -1 shape/argument violation,
+// -2 launch error.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gnf4_hip.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+
+constexpr int kNF4 = GNF4_FMT_NF4;
+constexpr int kMX = GNF4_FMT_MXFP4;
+
+// NF4 codebook, reference kernel/nf4_grouped.py:53-70 (code 7 is exactly 0).
+__constant__ float c_nf4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+    0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f,
+};
+
+// ---------------------------------------------------------------- decode --
+
+// The NF4 pair table: 256 bytes x 32 lane columns x float2 = 64 KiB. Declared
+// first so it sits at LDS offset 0 and the perm result is the full address.
+constexpr int kPairEntries = 256 * 32;
+
+__device__ __forceinline__ void init_pair_table(float2* tab) {
+  // thread t fills the 32 columns of byte t, rotating the column order by
+  // lane so one store instruction touches 64 distinct banks.
+  for (int b = threadIdx.x; b < 256; b += blockDim.x) {
+    const float2 v = make_float2(c_nf4[b >> 4], c_nf4[b & 15]);
+    for (int j = 0; j < 32; ++j) tab[b * 32 + ((j + b) & 31)] = v;
+  }
+}
+
+__device__ __forceinline__ unsigned bf16x2_bits(float lo, float hi) {
+  bf16x2_t r = {(__bf16)lo, (__bf16)hi};  // v_cvt_pk_bf16_f32, RNE
+  return __builtin_bit_cast(unsigned, r);
+}
+
+// 8 NF4 elements of one packed dword -> 4 dwords of bf16 pairs in k order.
+// lane_off = (lane % 32) * 8: the lane's private column in the pair table.
+__device__ __forceinline__ u32x4_t nf4_dword_to_bf16(const float2* tab, unsigned x,
+                                                     unsigned lane_off, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned addr = __builtin_amdgcn_perm(x, lane_off, 0x0C0C0000u | ((4u + i) << 8));
+    const float2 p = *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(tab) + addr);
+    r[i] = bf16x2_bits(p.x * s, p.y * s);
+  }
+  return r;
+}
+
+// 8 MXFP4 elements of one packed dword (low nibble first) -> 4 bf16 pairs.
+__device__ __forceinline__ u32x4_t mx_dword_to_bf16(unsigned x, float s) {
+  u32x4_t r;
+  r[0] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, s, 0));
+  r[1] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, s, 1));
+  r[2] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, s, 2));
+  r[3] = __builtin_bit_cast(unsigned, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, s, 3));
+  return r;
+}
+
+// e8m0 byte -> fp32 2^(e - 127): e = 0 is the subnormal 2^-127, e = 255 is
+// +inf (so a 0xFF block decodes to +-inf, and zero codes to NaN, like an
+// exp2-multiply decode; reference kernel/mxfp4_grouped.py:13-15).
+__device__ __forceinline__ float e8m0_to_f32(unsigned e) {
+  return __uint_as_float(e == 0 ? 0x00400000u : (e << 23));
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ f32x4_t mfma(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// Activation chunk (8 consecutive elements) as bf16 bits. fp16 inputs are
+// rejected on the host before launch; the kernels take bf16.
+__device__ __forceinline__ u32x4_t load_a8(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+
+// ============================================================ decode fwd ==
+
+struct FwdArgs {
+  const uint16_t* a;        // [T, lda] bf16
+  int64_t lda;
+  const uint8_t* B;         // [E, N, K/2]
+  int64_t sbe, sbn;         // bytes
+  const void* S;            // absmax f32 [E, N, K/64] or e8m0 u8 [E, N, K/32]
+  int64_t sse, ssn;         // elements
+  const int32_t* eids;      // [G]
+  const int32_t* row_off;   // [G + 1]
+  const int32_t* t_row0;    // [n_mtiles] (gemm path)
+  const int32_t* t_rows;
+  const int32_t* t_group;
+  int n_mtiles;
+  int G;
+  int64_t N, K;
+  uint16_t* out;            // [T, ldo] bf16
+  int64_t ldo;
+};
+
+constexpr int kDecodeWaves = 4;
+constexpr int kRing = 4;  // chunks in flight per wave (16 B weight + 64 B act per lane each)
+
+template <int FMT>
+__device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t n, int64_t k) {
+  if constexpr (FMT == kNF4) {
+    const float* s = static_cast<const float*>(p.S);
+    return s[e * p.sse + n * p.ssn + (k >> 6)];
+  } else {
+    const uint8_t* s = static_cast<const uint8_t*>(p.S);
+    return e8m0_to_f32(s[e * p.sse + n * p.ssn + (k >> 5)]);
+  }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
+  __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
+  if constexpr (FMT == kNF4) {
+    init_pair_table(s_tab);
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;   // weight row within the tile / activation row
+  const int q = lane >> 4;    // 32-element segment of a 128-element chunk
+  const unsigned lane_off = (unsigned)(lane & 31) * 8u;
+  const int64_t n_tiles = (p.N + 15) >> 4;
+  const int64_t units = (int64_t)p.G * n_tiles;
+  const int64_t nchunks = (p.K + 127) >> 7;
+
+  for (int64_t u = (int64_t)blockIdx.x * kDecodeWaves + wave; u < units;
+       u += (int64_t)gridDim.x * kDecodeWaves) {
+    const int g = (int)(u / n_tiles);
+    const int64_t nt = u - (int64_t)g * n_tiles;
+    const int r0 = p.row_off[g];
+    const int M = p.row_off[g + 1] - r0;
+    if (M <= 0) continue;
+    const int64_t e = p.eids[g];
+    const int64_t n = nt * 16 + nl;
+    const int64_t nc = n < p.N ? n : p.N - 1;
+    const uint8_t* brow = p.B + e * p.sbe + nc * p.sbn;
+    const bool mval = nl < M;
+    const uint16_t* arow = p.a + (int64_t)(r0 + (mval ? nl : 0)) * p.lda;
+
+    u32x4_t wb[kRing];
+    u32x4_t ab[kRing][4];
+    float sb[kRing];
+    auto issue = [&](int slot, int64_t c) {
+      const int64_t kseg = c * 128 + q * 32;
+      const bool kval = c < nchunks && kseg < p.K;
+      if (kval) {
+        wb[slot] = *reinterpret_cast<const u32x4_t*>(brow + (kseg >> 1));
+        sb[slot] = load_scale<FMT>(p, e, nc, kseg);
+      } else {
+        wb[slot] = u32x4_t{0u, 0u, 0u, 0u};
+        sb[slot] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ab[slot][j] = (kval && mval) ? load_a8(arow + kseg + 8 * j) : u32x4_t{0u, 0u, 0u, 0u};
+    };
+#pragma unroll
+    for (int s = 0; s < kRing; ++s) issue(s, s);
+
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t c0 = 0; c0 < nchunks; c0 += kRing) {
+#pragma unroll
+      for (int s = 0; s < kRing; ++s) {
+        const u32x4_t w = wb[s];
+        const float sc = sb[s];
+        u32x4_t a0 = ab[s][0], a1 = ab[s][1], a2 = ab[s][2], a3 = ab[s][3];
+        issue(s, c0 + s + kRing);
+        u32x4_t b0, b1, b2, b3;
+        if constexpr (FMT == kNF4) {
+          b0 = nf4_dword_to_bf16(s_tab, w[0], lane_off, sc);
+          b1 = nf4_dword_to_bf16(s_tab, w[1], lane_off, sc);
+          b2 = nf4_dword_to_bf16(s_tab, w[2], lane_off, sc);
+          b3 = nf4_dword_to_bf16(s_tab, w[3], lane_off, sc);
+        } else {
+          b0 = mx_dword_to_bf16(w[0], sc);
+          b1 = mx_dword_to_bf16(w[1], sc);
+          b2 = mx_dword_to_bf16(w[2], sc);
+          b3 = mx_dword_to_bf16(w[3], sc);
+        }
+        acc = mfma(a0, b0, acc);
+        acc = mfma(a1, b1, acc);
+        acc = mfma(a2, b2, acc);
+        acc = mfma(a3, b3, acc);
+      }
+    }
+    if (n < p.N) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * q + i;
+        if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(acc[i]);
+      }
+    }
+  }
+}
+
+// ============================================================ tiled GEMM ==
+
+constexpr int kLdsRow = 64 + 8;   // bf16 elements per staged row (16 B pad)
+constexpr int kBN = 128;          // forward n-tile
+constexpr int kThreads = 256;
+
+// Stage one 64-wide k-step of BM activation rows into LDS (zero-filled
+// outside [rows) x [K)). Each thread moves 16 B per pass.
+template <int BM>
+__device__ __forceinline__ void load_a_tile(u32x4_t (&r)[(BM * 8 + kThreads - 1) / kThreads],
+                                            const uint16_t* a, int64_t lda, int64_t row0,
+                                            int rows, int64_t k0, int64_t K) {
+  constexpr int P = (BM * 8 + kThreads - 1) / kThreads;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    const int rr = idx >> 3, kc = (idx & 7) * 8;
+    const bool ok = idx < BM * 8 && rr < rows && k0 + kc < K;
+    r[i] = ok ? load_a8(a + (row0 + rr) * lda + k0 + kc) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+}
+
+template <int BM>
+__device__ __forceinline__ void store_a_tile(const u32x4_t (&r)[(BM * 8 + kThreads - 1) / kThreads],
+                                             uint16_t* lds) {
+  constexpr int P = (BM * 8 + kThreads - 1) / kThreads;
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    if (idx < BM * 8) {
+      const int rr = idx >> 3, kc = (idx & 7) * 8;
+      *reinterpret_cast<u32x4_t*>(lds + rr * kLdsRow + kc) = r[i];
+    }
+  }
+}
+
+// Forward weight tile: kBN rows x 64 k = 32 packed bytes per row; thread t
+// owns row t / 2, bytes [16 (t % 2), +16) = 32 elements (one MX block, half an
+// NF4 block), so it needs exactly one scale.
+template <int FMT>
+struct BTileRegs {
+  u32x4_t w;
+  float s;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_b_fwd(BTileRegs<FMT>& r, const FwdArgs& p, int64_t e,
+                                           int64_t n0, int64_t k0) {
+  const int rr = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int64_t n = n0 + rr;
+  const int64_t k = k0 + half * 32;
+  if (n < p.N && k < p.K) {
+    r.w = *reinterpret_cast<const u32x4_t*>(p.B + e * p.sbe + n * p.sbn + (k >> 1));
+    r.s = load_scale<FMT>(p, e, n, k);
+  } else {
+    r.w = u32x4_t{0u, 0u, 0u, 0u};
+    r.s = 0.0f;
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void store_b_fwd(const BTileRegs<FMT>& r, const float2* tab,
+                                            uint16_t* lds) {
+  const int rr = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const unsigned lane_off = (unsigned)(threadIdx.x & 31) * 8u;
+  uint16_t* dst = lds + rr * kLdsRow + half * 32;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4_t v;
+    if constexpr (FMT == kNF4) v = nf4_dword_to_bf16(tab, r.w[i], lane_off, r.s);
+    else v = mx_dword_to_bf16(r.w[i], r.s);
+    *reinterpret_cast<u32x4_t*>(dst + 8 * i) = v;
+  }
+}
+
+// Waves: WM x WN = 4. Wave tile (BM / WM) x (BN / WN) in 16 x 16 MFMA tiles.
+template <int BM> struct WaveGrid { static constexpr int WM = BM >= 64 ? 2 : 1; };
+
+template <int FMT, int BM>
+__global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
+  constexpr int WM = WaveGrid<BM>::WM, WN = 4 / WM;
+  constexpr int MT = BM / WM / 16, NT = kBN / WN / 16;
+  constexpr int AP = (BM * 8 + kThreads - 1) / kThreads;
+  __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kLdsRow];
+  if constexpr (FMT == kNF4) init_pair_table(s_tab);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l16 = lane & 15, q = lane >> 4;
+  const int64_t n_tiles = (p.N + kBN - 1) / kBN;
+  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
+  const int64_t ksteps = (p.K + 63) >> 6;
+
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+    const int mt = (int)(t / n_tiles);
+    const int64_t n0 = (t - (int64_t)mt * n_tiles) * kBN;
+    const int64_t row0 = p.t_row0[mt];
+    const int rows = p.t_rows[mt];
+    const int64_t e = p.eids[p.t_group[mt]];
+
+    u32x4_t areg[AP];
+    BTileRegs<FMT> breg;
+    __syncthreads();  // previous tile's LDS readers are done (and table ready)
+    load_a_tile<BM>(areg, p.a, p.lda, row0, rows, 0, p.K);
+    load_b_fwd<FMT>(breg, p, e, n0, 0);
+    store_a_tile<BM>(areg, s_a[0]);
+    store_b_fwd<FMT>(breg, s_tab, s_b[0]);
+    __syncthreads();
+
+    f32x4_t acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t ks = 0; ks < ksteps; ++ks) {
+      const int cur = (int)(ks & 1);
+      const bool more = ks + 1 < ksteps;
+      if (more) {
+        load_a_tile<BM>(areg, p.a, p.lda, row0, rows, (ks + 1) * 64, p.K);
+        load_b_fwd<FMT>(breg, p, e, n0, (ks + 1) * 64);
+      }
+      const uint16_t* la = s_a[cur];
+      const uint16_t* lb = s_b[cur];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4_t bop[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          bop[j] = *reinterpret_cast<const u32x4_t*>(
+              lb + ((wn * NT + j) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const u32x4_t aop = *reinterpret_cast<const u32x4_t*>(
+              la + ((wm * MT + i) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[i][j] = mfma(aop, bop[j], acc[i][j]);
+        }
+      }
+      if (more) {
+        store_a_tile<BM>(areg, s_a[cur ^ 1]);
+        store_b_fwd<FMT>(breg, s_tab, s_b[cur ^ 1]);
+      }
+      __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t n = n0 + (wn * NT + j) * 16 + l16;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = (wm * MT + i) * 16 + 4 * q + r;
+          if (m < rows) p.out[(row0 + m) * p.ldo + n] = f32_to_bf16_bits(acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ================================================================= dgrad ==
+
+struct DgradArgs {
+  const uint16_t* g;        // [T, ldg] bf16 (grad_out)
+  int64_t ldg;
+  const uint8_t* B;
+  int64_t sbe, sbn;
+  const void* S;
+  int64_t sse, ssn;
+  const int32_t* eids;
+  const int32_t* t_row0;
+  const int32_t* t_rows;
+  const int32_t* t_group;
+  int n_mtiles;
+  int64_t N, K;
+  uint16_t* out;            // [T, ldo] bf16
+  int64_t ldo;
+};
+
+constexpr int kDgBK = 128;  // output k-tile
+
+// Weight tile for one 64-wide n-step: 64 rows x kDgBK k. Thread t owns rows
+// 4 (t / 16) .. +3 and k-elements [8 (t % 16), +8): four packed dwords, one
+// scale per row. Stored k-major (transposed) so the MFMA B operand (8
+// consecutive n for one k) is a single 16-byte LDS read.
+template <int FMT>
+struct DgRegs {
+  unsigned w[4];
+  float s[4];
+};
+
+template <int FMT>
+__device__ __forceinline__ float dg_scale(const DgradArgs& p, int64_t e, int64_t n, int64_t k) {
+  if constexpr (FMT == kNF4) {
+    return static_cast<const float*>(p.S)[e * p.sse + n * p.ssn + (k >> 6)];
+  } else {
+    return e8m0_to_f32(static_cast<const uint8_t*>(p.S)[e * p.sse + n * p.ssn + (k >> 5)]);
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_b_dg(DgRegs<FMT>& r, const DgradArgs& p, int64_t e,
+                                          int64_t n0, int64_t k0) {
+  const int rg = threadIdx.x >> 4, kc = threadIdx.x & 15;
+  const int64_t k = k0 + kc * 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + rg * 4 + i;
+    if (n < p.N && k < p.K) {
+      r.w[i] = *reinterpret_cast<const unsigned*>(p.B + e * p.sbe + n * p.sbn + (k >> 1));
+      r.s[i] = dg_scale<FMT>(p, e, n, k);
+    } else {
+      r.w[i] = 0u;
+      r.s[i] = 0.0f;
+    }
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ void store_b_dg(const DgRegs<FMT>& r, const float2* tab,
+                                           uint16_t* lds) {
+  const int rg = threadIdx.x >> 4, kc = threadIdx.x & 15;
+  const unsigned lane_off = (unsigned)(threadIdx.x & 31) * 8u;
+  u32x4_t rowv[4];  // per row: 8 elements as 4 bf16 pairs
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (FMT == kNF4) rowv[i] = nf4_dword_to_bf16(tab, r.w[i], lane_off, r.s[i]);
+    else rowv[i] = mx_dword_to_bf16(r.w[i], r.s[i]);
+  }
+  // transpose 4 rows x 8 k -> 8 k-rows of 4 consecutive n (8 bytes each)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // pair j holds k = 2j (low half) and 2j+1 (high half) of each row
+    const unsigned r0 = rowv[0][j], r1 = rowv[1][j], r2 = rowv[2][j], r3 = rowv[3][j];
+    const unsigned lo01 = __builtin_amdgcn_perm(r1, r0, 0x05040100u);  // k=2j: rows 0,1
+    const unsigned lo23 = __builtin_amdgcn_perm(r3, r2, 0x05040100u);
+    const unsigned hi01 = __builtin_amdgcn_perm(r1, r0, 0x07060302u);  // k=2j+1
+    const unsigned hi23 = __builtin_amdgcn_perm(r3, r2, 0x07060302u);
+    const int k_lo = kc * 8 + 2 * j;
+    *reinterpret_cast<uint2*>(lds + k_lo * kLdsRow + rg * 4) = make_uint2(lo01, lo23);
+    *reinterpret_cast<uint2*>(lds + (k_lo + 1) * kLdsRow + rg * 4) = make_uint2(hi01, hi23);
+  }
+}
+
+template <int FMT, int BM>
+__global__ void __launch_bounds__(kThreads, 1) k_gemm_dgrad(const DgradArgs p) {
+  constexpr int WM = WaveGrid<BM>::WM, WN = 4 / WM;
+  constexpr int MT = BM / WM / 16, NT = kDgBK / WN / 16;
+  constexpr int AP = (BM * 8 + kThreads - 1) / kThreads;
+  __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kDgBK * kLdsRow];
+  if constexpr (FMT == kNF4) init_pair_table(s_tab);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l16 = lane & 15, q = lane >> 4;
+  const int64_t k_tiles = (p.K + kDgBK - 1) / kDgBK;
+  const int64_t total = (int64_t)p.n_mtiles * k_tiles;
+  const int64_t nsteps = (p.N + 63) >> 6;
+
+  for (int64_t t = blockIdx.x; t < total; t += gridDim.x) {
+    const int mt = (int)(t / k_tiles);
+    const int64_t k0 = (t - (int64_t)mt * k_tiles) * kDgBK;
+    const int64_t row0 = p.t_row0[mt];
+    const int rows = p.t_rows[mt];
+    const int64_t e = p.eids[p.t_group[mt]];
+
+    u32x4_t areg[AP];
+    DgRegs<FMT> breg;
+    __syncthreads();
+    load_a_tile<BM>(areg, p.g, p.ldg, row0, rows, 0, p.N);
+    load_b_dg<FMT>(breg, p, e, 0, k0);
+    store_a_tile<BM>(areg, s_a[0]);
+    store_b_dg<FMT>(breg, s_tab, s_b[0]);
+    __syncthreads();
+
+    f32x4_t acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t ns = 0; ns < nsteps; ++ns) {
+      const int cur = (int)(ns & 1);
+      const bool more = ns + 1 < nsteps;
+      if (more) {
+        load_a_tile<BM>(areg, p.g, p.ldg, row0, rows, (ns + 1) * 64, p.N);
+        load_b_dg<FMT>(breg, p, e, (ns + 1) * 64, k0);
+      }
+      const uint16_t* la = s_a[cur];
+      const uint16_t* lb = s_b[cur];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4_t bop[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          bop[j] = *reinterpret_cast<const u32x4_t*>(
+              lb + ((wn * NT + j) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const u32x4_t aop = *reinterpret_cast<const u32x4_t*>(
+              la + ((wm * MT + i) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) acc[i][j] = mfma(aop, bop[j], acc[i][j]);
+        }
+      }
+      if (more) {
+        store_a_tile<BM>(areg, s_a[cur ^ 1]);
+        store_b_dg<FMT>(breg, s_tab, s_b[cur ^ 1]);
+      }
+      __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int64_t k = k0 + (wn * NT + j) * 16 + l16;
+        if (k >= p.K) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = (wm * MT + i) * 16 + 4 * q + r;
+          if (m < rows) p.out[(row0 + m) * p.ldo + k] = f32_to_bf16_bits(acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ================================================================== host ==
+
+struct DevInfo {
+  int cus = 0;
+};
+
+DevInfo g_dev[64];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (g_dev[dev].cus == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    g_dev[dev].cus = cus;
+  }
+  return g_dev[dev].cus;
+}
+
+int64_t clamp_grid(int64_t work, int64_t cap) { return work < cap ? (work > 0 ? work : 1) : cap; }
+
+template <int FMT>
+int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  if (p.n_mtiles == 0) {
+    // decode path: units = G x ceil(N / 16), 4 per workgroup, 2 workgroups/CU
+    const int64_t units = (int64_t)p.G * ((p.N + 15) / 16);
+    const int64_t grid = clamp_grid((units + kDecodeWaves - 1) / kDecodeWaves, (int64_t)cus * 2);
+    hipLaunchKernelGGL(k_decode_fwd<FMT>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+  } else {
+    const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kBN - 1) / kBN);
+    const int64_t grid = clamp_grid(tiles, cus);
+    switch (block_m) {
+      case 16: hipLaunchKernelGGL((k_gemm_fwd<FMT, 16>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+      case 32: hipLaunchKernelGGL((k_gemm_fwd<FMT, 32>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+      case 64: hipLaunchKernelGGL((k_gemm_fwd<FMT, 64>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+      case 128: hipLaunchKernelGGL((k_gemm_fwd<FMT, 128>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+      default: return -1;
+    }
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+template <int FMT>
+int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  const int64_t tiles = (int64_t)p.n_mtiles * ((p.K + kDgBK - 1) / kDgBK);
+  const int64_t grid = clamp_grid(tiles, cus);
+  switch (block_m) {
+    case 16: hipLaunchKernelGGL((k_gemm_dgrad<FMT, 16>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+    case 32: hipLaunchKernelGGL((k_gemm_dgrad<FMT, 32>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+    case 64: hipLaunchKernelGGL((k_gemm_dgrad<FMT, 64>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+    case 128: hipLaunchKernelGGL((k_gemm_dgrad<FMT, 128>), dim3((unsigned)grid), dim3(kThreads), 0, stream, p); break;
+    default: return -1;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+// ============================================================== C ABI ====
+
+extern "C" {
+
+int gnf4_hip_abi_version(void) { return GNF4_HIP_ABI_VERSION; }
+
+int gnf4_hip_device_cus(void) { return device_cus(); }
+
+int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,
+                         int64_t stride_be, int64_t stride_bn, const void* scales,
+                         int64_t stride_se, int64_t stride_sn, const int32_t* expert_ids,
+                         const int32_t* row_off, int G, const int32_t* t_row0,
+                         const int32_t* t_rows, const int32_t* t_group, int n_mtiles,
+                         int block_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                         void* stream) {
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk || G < 0 || n_mtiles < 0) return -1;
+  if (!a || !B || !scales || !expert_ids || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  if (n_mtiles == 0 && !row_off) return -1;
+  if (n_mtiles > 0 && (!t_row0 || !t_rows || !t_group)) return -1;
+  FwdArgs p;
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.row_off = row_off;
+  p.t_row0 = t_row0;
+  p.t_rows = t_rows;
+  p.t_group = t_group;
+  p.n_mtiles = n_mtiles;
+  p.G = G;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  if (n_mtiles == 0 && G == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, block_m, s) : launch_fwd<kMX>(p, block_m, s);
+}
+
+int gnf4_hip_nf4_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* B,
+                     int64_t stride_be, int64_t stride_bn, const float* absmax,
+                     int64_t stride_ae, int64_t stride_an, const int32_t* expert_ids,
+                     const int32_t* row_off, int G, const int32_t* t_row0,
+                     const int32_t* t_rows, const int32_t* t_group, int n_mtiles, int block_m,
+                     int64_t N, int64_t K, void* out, int64_t ldo, void* stream) {
+  return gnf4_hip_grouped_fwd(GNF4_FMT_NF4, a, a_dtype, lda, B, stride_be, stride_bn, absmax,
+                              stride_ae, stride_an, expert_ids, row_off, G, t_row0, t_rows,
+                              t_group, n_mtiles, block_m, N, K, out, ldo, stream);
+}
+
+int gnf4_hip_mxfp4_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* blocks,
+                       int64_t stride_be, int64_t stride_bn, const uint8_t* scales,
+                       int64_t stride_se, int64_t stride_sn, const int32_t* expert_ids,
+                       const int32_t* row_off, int G, const int32_t* t_row0,
+                       const int32_t* t_rows, const int32_t* t_group, int n_mtiles,
+                       int block_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                       void* stream) {
+  return gnf4_hip_grouped_fwd(GNF4_FMT_MXFP4, a, a_dtype, lda, blocks, stride_be, stride_bn,
+                              scales, stride_se, stride_sn, expert_ids, row_off, G, t_row0,
+                              t_rows, t_group, n_mtiles, block_m, N, K, out, ldo, stream);
+}
+
+int gnf4_hip_grouped_dgrad(int fmt, const void* grad_out, int g_dtype, int64_t ldg,
+                           const uint8_t* B, int64_t stride_be, int64_t stride_bn,
+                           const void* scales, int64_t stride_se, int64_t stride_sn,
+                           const int32_t* expert_ids, const int32_t* t_row0,
+                           const int32_t* t_rows, const int32_t* t_group, int n_mtiles,
+                           int block_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                           void* stream) {
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || g_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk || n_mtiles < 0) return -1;
+  if (!grad_out || !B || !scales || !expert_ids || !out) return -1;
+  if (n_mtiles > 0 && (!t_row0 || !t_rows || !t_group)) return -1;
+  if (ldg < N || ldg % 8 || ldo < K || stride_bn % 4 || stride_be % 4 || !aligned16(grad_out) ||
+      (reinterpret_cast<uintptr_t>(B) & 3))
+    return -1;
+  if (n_mtiles == 0) return 0;
+  DgradArgs p;
+  p.g = static_cast<const uint16_t*>(grad_out);
+  p.ldg = ldg;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.t_row0 = t_row0;
+  p.t_rows = t_rows;
+  p.t_group = t_group;
+  p.n_mtiles = n_mtiles;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_dgrad<kNF4>(p, block_m, s)
+                             : launch_dgrad<kMX>(p, block_m, s);
+}
+
+int gnf4_hip_nf4_dgrad(const void* grad_out, int g_dtype, int64_t ldg, const uint8_t* B,
+                       int64_t stride_be, int64_t stride_bn, const float* absmax,
+                       int64_t stride_ae, int64_t stride_an, const int32_t* expert_ids,
+                       const int32_t* t_row0, const int32_t* t_rows, const int32_t* t_group,
+                       int n_mtiles, int block_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                       void* stream) {
+  return gnf4_hip_grouped_dgrad(GNF4_FMT_NF4, grad_out, g_dtype, ldg, B, stride_be, stride_bn,
+                                absmax, stride_ae, stride_an, expert_ids, t_row0, t_rows,
+                                t_group, n_mtiles, block_m, N, K, out, ldo, stream);
+}
+
+int gnf4_hip_mxfp4_dgrad(const void* grad_out, int g_dtype, int64_t ldg, const uint8_t* blocks,
+                         int64_t stride_be, int64_t stride_bn, const uint8_t* scales,
+                         int64_t stride_se, int64_t stride_sn, const int32_t* expert_ids,
+                         const int32_t* t_row0, const int32_t* t_rows, const int32_t* t_group,
+                         int n_mtiles, int block_m, int64_t N, int64_t K, void* out,
+                         int64_t ldo, void* stream) {
+  return gnf4_hip_grouped_dgrad(GNF4_FMT_MXFP4, grad_out, g_dtype, ldg, blocks, stride_be,
+                                stride_bn, scales, stride_se, stride_sn, expert_ids, t_row0,
+                                t_rows, t_group, n_mtiles, block_m, N, K, out, ldo, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,603 @@
+"""Grouped W4A16 GEMM over NF4 expert stacks on MI355X (gfx950), dequant fused.
+
+Drop-in for the reference module of the same name (kernel/nf4_grouped.py):
+same entry points, keyword arguments, exported helpers and error behaviour.
+
+``gemm_4bit_grouped`` computes, in one launch for all active experts,
+``out[t, :] = a[t, :] @ dequant_nf4(B[e(t)]).T`` for tokens grouped by expert;
+``dgrad_4bit_grouped`` is its backward with respect to the activations. The
+packed ``[E, N, K/2]`` bytes are decoded inside the kernel and never written
+back to memory. Both call hand-written HIP kernels (``csrc/gnf4_hip.hip``)
+through the C ABI in ``include/gnf4_hip.h``; there is no CPU, Triton or
+eager-PyTorch fallback. On a non-GPU tensor the ops raise.
+
+Numerics: every weight is decoded as ``bf16(fp32(NF4[code] * absmax))`` (one
+fp32 rounding, one bf16 rounding -- the same values ``dequant_ref(...)`` gives
+after ``.to(bfloat16)``), products are exact in the bf16 MFMA and accumulate
+in fp32, and each output is rounded to bf16 once. The reference's Triton
+mainloop uses TF32 operands instead; the stated bound is the tolerance
+contract (reference docs/TOLERANCE_CONTRACT.md): B-rel <= 2x the bf16
+dequant-then-matmul path against an fp64 reference, and <= 1e-2.
+"""
+from __future__ import annotations
+
+import os
+import threading
+
+import torch
+
+import _hiplib
+
+# The NF4 codebook (reference kernel/nf4_grouped.py:53-70). Code 7 is exactly 0.
+NF4_LUT = [
+    -1.0,
+    -0.6961928009986877,
+    -0.5250730514526367,
+    -0.39491748809814453,
+    -0.28444138169288635,
+    -0.18477343022823334,
+    -0.09105003625154495,
+    0.0,
+    0.07958029955625534,
+    0.16093020141124725,
+    0.24611230194568634,
+    0.33791524171829224,
+    0.44070982933044434,
+    0.5626170039176941,
+    0.7229568362236023,
+    1.0,
+]
+BLOCKSIZE = 64  # quant blocksize; K % 64 == 0 enforced
+
+#: The reference gates its register-LUT mainloop on triton's ``tl.gather``.
+#: This build has one mainloop (LDS pair table + bf16 MFMA); the flag stays
+#: exported and True so callers that branch on it take the default path.
+HAS_TL_GATHER = True
+
+# Dispatch constants, kept with the reference's values and meaning
+# (kernel/nf4_grouped.py:593-607): the byte floor below which a product
+# integration should prefer the dequant path, and the per-split block floor
+# of the split-K plan.
+DECODE_MIN_FUSED_BYTES = 3_000_000
+SPLITK_MIN_BLOCKS = 32
+
+#: (BLOCK_M, BLOCK_N, BLOCK_K, num_warps) default of the dgrad launch
+#: (reference kernel/nf4_grouped.py:1031). Here only BLOCK_M selects a tile
+#: height; the contraction step is fixed, so no config changes output bits.
+_DGRAD_DEFAULT = (32, 64, 64, 2)
+
+#: Largest group the decode kernel takes (rows of one MFMA A tile).
+DECODE_MAX_ROWS = 16
+
+
+def repack_from_bnb(packed_list, states, N: int, K: int):
+    """bnb per-expert ``quantize_4bit`` output -> ``B [E, N, K//2] u8`` and
+    ``absmax [E, N, K//64] f32`` (reference kernel/nf4_grouped.py:74-96).
+    bnb stores both flat in row-major order, so they reshape when K % 64 == 0;
+    nested (compress_statistics) states are de-nested with bnb itself."""
+    assert K % BLOCKSIZE == 0, f"K={K} not a multiple of blocksize {BLOCKSIZE}"
+    E = len(packed_list)
+    dev = packed_list[0].device
+    B = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
+    A = torch.empty(E, N, K // BLOCKSIZE, dtype=torch.float32, device=dev)
+    for e in range(E):
+        B[e] = packed_list[e].reshape(N, K // 2)
+        st = states[e]
+        am = st.absmax
+        if getattr(st, "nested", False):
+            from bitsandbytes import functional as F
+
+            am = F.dequantize_blockwise(st.absmax, st.state2) + st.offset
+        A[e] = am.to(torch.float32).reshape(N, K // BLOCKSIZE)
+    return B, A
+
+
+# ------------------------------------------------------------------ indices --
+
+class _PinnedIndexArena:
+    """Pinned host staging for the small int32 index arrays, used while a
+    stream is being captured into a graph (reference kernel/nf4_grouped.py:
+    99-226). A pageable ``torch.tensor(list, device=...)`` synchronises, which
+    a capture forbids; a copy from pinned memory that already exists does not.
+    Slices taken under capture are owned forever -- replays re-read them -- so
+    the bump pointer never rewinds, and the arena refuses to grow inside a
+    capture. Size it with ``GNF4_PIN_ARENA_INTS`` or ``reserve()``."""
+
+    DEFAULT_INTS = int(os.environ.get("GNF4_PIN_ARENA_INTS", 1 << 20))
+
+    def __init__(self, device, n: int | None = None):
+        self.device = device
+        self.host = torch.empty(n or self.DEFAULT_INTS, dtype=torch.int32, pin_memory=True)
+        self.off = 0
+        self._retired: list = []
+
+    @staticmethod
+    def _capturing() -> bool:
+        try:
+            return torch.cuda.is_current_stream_capturing()
+        except Exception:
+            return False
+
+    def take(self, n: int):
+        capturing = self._capturing()
+        if self.off + n > self.host.numel():
+            if capturing:
+                raise RuntimeError(
+                    "grouped-nf4: the pinned index arena (%d int32, %d owned by "
+                    "earlier captures) cannot hold %d more ints, and growing it "
+                    "would allocate pinned memory inside the capture. Set "
+                    "GNF4_PIN_ARENA_INTS to at least %d, or call reserve() "
+                    "before capturing." % (self.host.numel(), self.off, n, 2 * (self.off + n)))
+            self._grow(self.off + n)
+        view = self.host[self.off:self.off + n]
+        self.off += n
+        return view, capturing
+
+    def _grow(self, need: int):
+        self._retired.append(self.host)       # live graphs may still read it
+        fresh = torch.empty(max(2 * self.host.numel(), need), dtype=torch.int32,
+                            pin_memory=True)
+        fresh[: self.off] = self.host[: self.off]
+        self.host = fresh
+
+    def reserve(self, n_more: int):
+        if self._capturing():
+            raise RuntimeError("reserve() inside a capture would allocate pinned "
+                               "memory in the region; call it before capturing.")
+        if self.off + n_more > self.host.numel():
+            self._grow(self.off + n_more)
+
+    def mark(self):
+        """Kept for call-site compatibility; nothing rewinds, nothing waits."""
+
+
+class _PinnedRing:
+    """Outside capture: a small ring of pinned staging buffers, each guarded
+    by an event, so an index upload is an asynchronous copy that never stalls
+    the host on the GPU (the reference's pageable copy synchronises)."""
+
+    SLOTS = 8
+
+    def __init__(self):
+        self.slots = [None] * self.SLOTS
+        self.events = [None] * self.SLOTS
+        self.i = 0
+        self.lock = threading.Lock()
+
+    def stage(self, flat: list, dev):
+        with self.lock:
+            i = self.i
+            self.i = (i + 1) % self.SLOTS
+            ev = self.events[i]
+            if ev is not None:
+                ev.synchronize()              # the copy that last used this slot
+            buf = self.slots[i]
+            n = len(flat)
+            if buf is None or buf.numel() < n:
+                buf = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
+                self.slots[i] = buf
+            host = buf[:n]
+            host.copy_(torch.tensor(flat, dtype=torch.int32))
+            out = host.to(dev, non_blocking=True)
+            if ev is None:
+                ev = torch.cuda.Event()
+                self.events[i] = ev
+            ev.record(torch.cuda.current_stream(dev))
+            return out
+
+
+_ARENAS: dict = {}
+_RINGS: dict = {}
+
+
+def _arena(device) -> _PinnedIndexArena:
+    key = str(device)
+    if key not in _ARENAS:
+        _ARENAS[key] = _PinnedIndexArena(device)
+    return _ARENAS[key]
+
+
+def _ring(device) -> _PinnedRing:
+    key = str(device)
+    if key not in _RINGS:
+        _RINGS[key] = _PinnedRing()
+    return _RINGS[key]
+
+
+def to_device_i32(seqs, device):
+    """Small host integer sequences (lists or CPU tensors) to int32 device
+    views, in one transfer; one view per input, in order, identical values on
+    every path (reference kernel/nf4_grouped.py:229-331). Under graph capture
+    the transfer stages through the permanent pinned arena; otherwise through
+    an event-guarded pinned ring (asynchronous, no host sync)."""
+    lens = [len(s) for s in seqs]
+    total = sum(lens)
+    dev = torch.device(device)
+    if total == 0:
+        return [torch.empty(0, dtype=torch.int32, device=dev) for _ in seqs]
+    flat = [int(v) for s in seqs for v in (s.tolist() if torch.is_tensor(s) else s)]
+    cuda = dev.type == "cuda" and torch.cuda.is_available()
+    if not cuda:
+        packed = torch.tensor(flat, dtype=torch.int32, device=dev)
+    else:
+        ar = _arena(dev)   # exists before any capture starts
+        capturing = ar._capturing()
+        if capturing:
+            host, _ = ar.take(total)
+            host.copy_(torch.tensor(flat, dtype=torch.int32))
+            packed = host.to(dev, non_blocking=True)
+        else:
+            packed = _ring(dev).stage(flat, dev)
+    out, off = [], 0
+    for n in lens:
+        out.append(packed[off:off + n])
+        off += n
+    return out
+
+
+def _tiles_host(sizes, block_m: int):
+    """(t_row0, t_rows, t_group) lists: each group cut into block_m-row tiles;
+    empty groups emit nothing. ``sizes`` is only read (``int(m)`` keeps a
+    tensor argument from being decremented in place, reference
+    kernel/nf4_grouped.py:334-346)."""
+    t_row0, t_rows, t_group = [], [], []
+    row = 0
+    for g, m in enumerate(sizes):
+        m = int(m)
+        r = 0
+        while r < m:
+            take = min(block_m, m - r)
+            t_row0.append(row + r)
+            t_rows.append(take)
+            t_group.append(g)
+            r += take
+        row += m
+    return t_row0, t_rows, t_group
+
+
+def build_group_tiles(sizes, block_m: int, device):
+    """Expand jagged group sizes into fixed M-tiles: ``(row0, valid_rows,
+    group_idx)`` int32 device tensors, one transfer for all three
+    (reference kernel/nf4_grouped.py:334-362)."""
+    a, b, c = to_device_i32(_tiles_host(sizes, block_m), device)
+    return a, b, c
+
+
+# --------------------------------------------------------------------- plan --
+
+_LUT_CACHE: dict = {}
+_SM_CACHE: dict = {}
+
+
+def _sm_count(device) -> int:
+    """Compute-unit count of ``device`` (the reference's SM count query,
+    kernel/nf4_grouped.py:581-591); 64 when no GPU is visible."""
+    key = str(device)
+    if key not in _SM_CACHE:
+        if torch.cuda.is_available() and "cuda" in key:
+            _SM_CACHE[key] = torch.cuda.get_device_properties(device).multi_processor_count
+        else:
+            _SM_CACHE[key] = 64
+    return _SM_CACHE[key]
+
+
+def _decode_plan(N: int, K: int, T: int, sm_count: int):
+    """Decode plan ``(BLOCK_N, num_warps, split_k)`` with the reference's rule
+    (kernel/nf4_grouped.py:609-632): the constant (64, 2) and split-K only for
+    starved grids (programs < 2 * SMs), power of two up to 8, each split owning
+    at least SPLITK_MIN_BLOCKS absmax blocks. The HIP decode kernel streams
+    whole rows per wave and does not use the numbers; the function is kept for
+    callers and for ``decode_dispatch``."""
+    bn, warps = 64, 2
+    programs = T * -(-N // bn)
+    split_k = 1
+    if programs < 2 * sm_count:
+        want = -(-(4 * sm_count) // programs)
+        while split_k < want and split_k < 8:
+            split_k *= 2
+        kblocks = max(K // BLOCKSIZE, 1)
+        while split_k > 1 and kblocks // split_k < SPLITK_MIN_BLOCKS:
+            split_k //= 2
+    return bn, warps, split_k
+
+
+def decode_dispatch(N: int, K: int, T: int, sm_count: int):
+    """``("dequant",)`` below the fused floor, else ``("fused", BLOCK_N,
+    num_warps, split_k)`` (reference kernel/nf4_grouped.py:635-649). The op
+    itself always runs fused; integrations consult this helper."""
+    traffic = T * N * (K // 2 + K // 16)
+    if traffic < DECODE_MIN_FUSED_BYTES:
+        return ("dequant",)
+    return ("fused", *_decode_plan(N, K, T, sm_count))
+
+
+def _lut(device):
+    key = str(device)
+    if key not in _LUT_CACHE:
+        _LUT_CACHE[key] = torch.tensor(NF4_LUT, dtype=torch.float32, device=device)
+    return _LUT_CACHE[key]
+
+
+def _prefill_block_m(max_rows: int) -> int:
+    """Group-size-keyed M-tile height (reference kernel/nf4_grouped.py:686-694)."""
+    if max_rows <= 16:
+        return 16
+    if max_rows <= 32:
+        return 32
+    if max_rows <= 64:
+        return 64
+    return 128
+
+
+_SUPPORTED_BLOCK_M = (16, 32, 64, 128)
+
+
+def _kernel_block_m(block_m: int) -> int:
+    """The smallest supported tile height >= block_m (tiling never changes
+    what an output row is, only how rows are batched)."""
+    for bm in _SUPPORTED_BLOCK_M:
+        if block_m <= bm:
+            return bm
+    return 128
+
+
+# ------------------------------------------------------------------ launch --
+
+def _require_gpu(t: torch.Tensor, op: str, hint: str):
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{op} runs the HIP kernel and requires CUDA tensors (ROCm devices "
+            f"report type 'cuda'; got device '{t.device.type}'). {hint}")
+
+
+def _aligned_rows(t: torch.Tensor, align: int) -> torch.Tensor:
+    """Packed weights with a contiguous last dimension and row/expert strides
+    (and base) aligned to ``align`` bytes; a misaligned view is copied."""
+    if (t.stride(-1) != 1 or t.stride(1) % align or t.stride(0) % align
+            or t.data_ptr() % align):
+        return t.contiguous()
+    return t
+
+
+def _scales_view(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _act_view(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1 or t.stride(0) % 8 or t.data_ptr() % 16:
+        return t.contiguous()
+    return t
+
+
+def _eids_device(expert_ids, dev):
+    """Expert ids as int32 on ``dev``: a device tensor passes through; a list
+    or host tensor converts once (same values on every path)."""
+    if torch.is_tensor(expert_ids) and expert_ids.is_cuda:
+        return expert_ids.to(device=dev, dtype=torch.int32)
+    return None
+
+
+def _stream_ptr(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
+    """Shared forward launcher for NF4 and MXFP4."""
+    lib = _hiplib.load()
+    E, N, half = W.shape
+    T, K = a_cat.shape
+    dev = a_cat.device
+    out = torch.empty(T, N, dtype=torch.bfloat16, device=dev)
+    G = len(sizes)
+    if T == 0 or G == 0:
+        return out
+    if a_cat.dtype != torch.bfloat16:
+        raise TypeError(f"{op}: activations must be bfloat16 in this build, got {a_cat.dtype}")
+    a_cat = _act_view(a_cat)
+    W = _aligned_rows(W, 16)
+    S = _scales_view(S)
+    sizes_i = [int(m) for m in sizes]
+    max_m = max(sizes_i)
+    eids_dev = _eids_device(expert_ids, dev)
+    host_eids = [] if eids_dev is not None else expert_ids
+    if max_m <= DECODE_MAX_ROWS and block_m is None:
+        row_off = [0]
+        for m in sizes_i:
+            row_off.append(row_off[-1] + m)
+        e_h, r_h = to_device_i32((host_eids, row_off), dev)
+        eids = eids_dev if eids_dev is not None else e_h
+        args = (eids.data_ptr(), r_h.data_ptr(), G, None, None, None, 0, 0)
+        keep = (e_h, r_h, eids)
+    else:
+        bm = _kernel_block_m(block_m if block_m is not None else _prefill_block_m(max_m))
+        t0, tr, tg = _tiles_host(sizes_i, bm)
+        e_h, t0_d, tr_d, tg_d = to_device_i32((host_eids, t0, tr, tg), dev)
+        eids = eids_dev if eids_dev is not None else e_h
+        args = (eids.data_ptr(), None, G, t0_d.data_ptr(), tr_d.data_ptr(),
+                tg_d.data_ptr(), len(t0), bm)
+        keep = (e_h, t0_d, tr_d, tg_d, eids)
+    with torch.cuda.device(dev):
+        rc = lib.gnf4_hip_grouped_fwd(
+            fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+            W.data_ptr(), W.stride(0), W.stride(1),
+            S.data_ptr(), S.stride(0), S.stride(1),
+            *args, N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    del keep  # index tensors stay alive until the launch is enqueued
+    _hiplib.check(rc, op)
+    return out
+
+
+def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, block_m, op):
+    lib = _hiplib.load()
+    E, N, half = W.shape
+    K = half * 2
+    T = grad_out.shape[0]
+    dev = grad_out.device
+    out = torch.empty(T, K, dtype=torch.bfloat16, device=dev)
+    G = len(sizes)
+    if T == 0 or G == 0:
+        return out
+    g = _act_view(grad_out)
+    W = _aligned_rows(W, 4)
+    S = _scales_view(S)
+    bm = _kernel_block_m(block_m)
+    t0, tr, tg = _tiles_host([int(m) for m in sizes], bm)
+    eids_dev = _eids_device(expert_ids, dev)
+    e_h, t0_d, tr_d, tg_d = to_device_i32(([] if eids_dev is not None else expert_ids,
+                                           t0, tr, tg), dev)
+    eids = eids_dev if eids_dev is not None else e_h
+    with torch.cuda.device(dev):
+        rc = lib.gnf4_hip_grouped_dgrad(
+            fmt, g.data_ptr(), _hiplib.DTYPE_BF16, g.stride(0),
+            W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+            eids.data_ptr(), t0_d.data_ptr(), tr_d.data_ptr(), tg_d.data_ptr(), len(t0), bm,
+            N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    _hiplib.check(rc, op)
+    return out
+
+
+# ------------------------------------------------------------------ forward --
+
+_PREFILL_VARIANTS = (0, 1, 3)
+
+
+def gemm_4bit_grouped(
+    a_cat,
+    B,
+    absmax,
+    sizes,
+    expert_ids,
+    block_m: int | None = None,
+    decode_config: tuple | None = None,
+    split_k: int | None = None,
+    prefill_config: tuple | None = None,
+    prefill_variant: int | None = None,
+    prefill_groups: int = 1,
+):
+    """Single-launch grouped NF4 GEMM (reference kernel/nf4_grouped.py:697-907).
+
+    ``a_cat [T, K]`` bf16, group-sorted; ``B [E, N, K//2]`` uint8;
+    ``absmax [E, N, K//64]`` fp32; ``sizes`` per-group row counts (a list or
+    tensor, read only; zero-size groups are allowed); ``expert_ids [G]`` as a
+    list, CPU tensor or device tensor (all give identical bits). Returns
+    ``[T, N]`` bf16 in the same group order.
+
+    Path: groups of at most 16 rows (always when ``max(sizes) == 1``) take the
+    decode kernel, which streams each active expert's weights once; larger
+    groups take the tiled MFMA kernel with ``block_m`` (default
+    ``_prefill_block_m(max(sizes))``). An explicit ``block_m`` forces the tiled
+    kernel for groups above one row.
+
+    The reference's tuning knobs are accepted and validated so call sites keep
+    working: ``decode_config`` (BLOCK_N, num_warps), ``split_k`` (>= 1),
+    ``prefill_config`` (BLOCK_N, num_warps, num_stages), ``prefill_variant``
+    (0, 1 or 3) and ``prefill_groups`` (1 or 2). They select Triton schedules
+    in the reference; here one HIP mainloop serves them all and they change
+    neither the path nor the result.
+    """
+    E, N, _ = B.shape
+    T, K = a_cat.shape
+    assert sum(int(m) for m in sizes) == T, (sum(int(m) for m in sizes), T)
+    dev = a_cat.device
+    _require_gpu(
+        a_cat, "gemm_4bit_grouped",
+        "For a CPU-checkable decode of the same NF4 bytes, use "
+        "dequant_ref(packed, absmax, N, K) -- the pure-torch reference decode.")
+    if B.dtype != torch.uint8:
+        raise TypeError(f"B must be uint8 packed nibbles, got {B.dtype}")
+    if absmax.dtype != torch.float32:
+        raise TypeError(f"absmax must be float32, got {absmax.dtype}")
+    if K % BLOCKSIZE or B.shape[2] * 2 != K:
+        raise ValueError(f"K={K} must equal 2*B.shape[2]={2 * B.shape[2]} and be a "
+                         f"multiple of {BLOCKSIZE}")
+    if tuple(absmax.shape) != (E, N, K // BLOCKSIZE):
+        raise ValueError(f"absmax shape {tuple(absmax.shape)} != {(E, N, K // BLOCKSIZE)}")
+    if len(sizes) != len(expert_ids):
+        raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
+    if decode_config is not None and len(tuple(decode_config)) != 2:
+        raise ValueError(f"decode_config must be (BLOCK_N, num_warps), got {decode_config}")
+    if split_k is not None and int(split_k) < 1:
+        raise ValueError(f"split_k must be >= 1, got {split_k}")
+    if prefill_config is not None and len(tuple(prefill_config)) != 3:
+        raise ValueError("prefill_config must be (BLOCK_N, num_warps, num_stages), "
+                         f"got {prefill_config}")
+    if prefill_variant is not None and prefill_variant not in _PREFILL_VARIANTS:
+        raise ValueError(f"prefill_variant {prefill_variant} is not one of {_PREFILL_VARIANTS}")
+    if prefill_groups not in (1, 2):
+        raise ValueError(f"prefill_groups must be 1 or 2, got {prefill_groups}")
+    if prefill_groups == 2 and K % (2 * BLOCKSIZE):
+        raise ValueError(f"prefill_groups=2 needs K % {2 * BLOCKSIZE} == 0, got K={K}")
+    if B.device != dev or absmax.device != dev:
+        raise ValueError("a_cat, B and absmax must be on the same device")
+    bm = block_m if (block_m is not None and max((int(m) for m in sizes), default=0) > 1) else None
+    return _launch_fwd(_hiplib.FMT_NF4, a_cat, B, absmax, sizes, expert_ids, bm,
+                       "gemm_4bit_grouped")
+
+
+def dequant_ref(packed_row_major: torch.Tensor, absmax: torch.Tensor, N: int, K: int):
+    """Pure-torch reference decode: ``w[n, k] = NF4[code] * absmax[n, k//64]``
+    in fp32, element 2j from the HIGH nibble (reference
+    kernel/nf4_grouped.py:910-929). Runs on any device; it is the checkable
+    decode the error messages point CPU callers to."""
+    lut = _lut(packed_row_major.device)
+    flat = packed_row_major.reshape(-1).to(torch.int32)
+    hi = (flat >> 4) & 0xF
+    lo = flat & 0xF
+    codes = torch.stack([hi, lo], dim=1).reshape(-1)
+    vals = lut[codes]
+    am = absmax.to(torch.float32).reshape(-1).repeat_interleave(BLOCKSIZE)
+    return (vals * am).reshape(N, K)
+
+
+# -------------------------------------------------------------------- dgrad --
+
+def dgrad_eligible(grad_out, B, absmax, block_k: int = 64):
+    """None if this problem can take the dgrad kernel, else the reason
+    (reference kernel/nf4_grouped.py:1034-1053)."""
+    if grad_out.dtype != torch.bfloat16:
+        return f"grad_out dtype {grad_out.dtype} is not bfloat16"
+    if BLOCKSIZE % block_k:
+        return f"BLOCK_K {block_k} does not divide the quant blocksize {BLOCKSIZE}"
+    K = B.shape[2] * 2
+    if K % block_k:
+        return f"K {K} not divisible by BLOCK_K {block_k}"
+    if absmax.shape[2] * BLOCKSIZE != K:
+        return f"absmax blocks {absmax.shape[2]} do not tile K {K} at blocksize {BLOCKSIZE}"
+    if B.numel() == 0:
+        return "packed storage is empty (evicted?)"
+    return None
+
+
+def dgrad_4bit_grouped(grad_out, B, absmax, sizes, expert_ids, config=None):
+    """``grad_a[t, :] = grad_out[t, :] @ dequant_nf4(B[e(t)])`` in one launch
+    (reference kernel/nf4_grouped.py:1056-1121). ``grad_out [T, N]`` bf16
+    group-sorted; returns ``[T, K]`` bf16. The weights are read through the
+    same ``[E, N, K/2]`` layout as the forward (no transposed copy).
+
+    ``config`` = (BLOCK_M, BLOCK_N, BLOCK_K, num_warps): BLOCK_K must divide
+    64 (eligibility); BLOCK_M picks the tile height. The contraction over N
+    runs in fixed ascending 64-wide steps whatever the config, so the output
+    is bitwise independent of it."""
+    E, N, half = B.shape
+    K = half * 2
+    T = grad_out.shape[0]
+    assert sum(int(m) for m in sizes) == T, (sum(int(m) for m in sizes), T)
+    _require_gpu(
+        grad_out, "dgrad_4bit_grouped",
+        "The CPU-checkable equivalent is grad_out @ dequant_ref(packed, absmax, N, K) "
+        "per group.")
+    block_m, _block_n, block_k, _warps = config or _DGRAD_DEFAULT
+    why = dgrad_eligible(grad_out, B, absmax, block_k)
+    if why is not None:
+        raise ValueError(
+            f"dgrad_4bit_grouped cannot run this problem: {why}. Callers that can "
+            "fall back should check dgrad_eligible() first rather than catching this.")
+    if grad_out.shape[1] != N:
+        raise ValueError(f"grad_out has {grad_out.shape[1]} columns, B has N={N}")
+    if absmax.dtype != torch.float32 or tuple(absmax.shape) != (E, N, K // BLOCKSIZE):
+        raise ValueError(f"absmax must be float32 {(E, N, K // BLOCKSIZE)}, got "
+                         f"{absmax.dtype} {tuple(absmax.shape)}")
+    if len(sizes) != len(expert_ids):
+        raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
+    return _launch_dgrad(_hiplib.FMT_NF4, grad_out, B, absmax, sizes, expert_ids,
+                         int(block_m), "dgrad_4bit_grouped")

@@ -1,0 +1,126 @@
+/* gnf4_hip.h -- C ABI of libgnf4_hip.so, the grouped 4-bit MoE expert GEMM
+ * for AMD Instinct MI355X (gfx950).
+ *
+ * Plain pointers and sizes only. All pointers are device pointers except
+ * `stream`, which is a hipStream_t (pass torch.cuda.current_stream().cuda_stream).
+ * Every call is asynchronous and stream-ordered; none allocates or synchronises.
+ *
+ * Shared conventions (reference docs/KERNEL_CONTRACT.md, kernel/nf4_grouped.py:697-725):
+ *   a / grad_out  [T, ld] bf16, rows sorted by group (group g owns rows
+ *                 row_off[g] .. row_off[g+1]); ld % 8 == 0, 16-byte aligned.
+ *   B / blocks    [E, N, K/2] uint8, last dimension contiguous; strides in
+ *                 BYTES, multiples of 16 (forward) / 4 (dgrad).
+ *   absmax        [E, N, K/64] fp32 (NF4, K % 64 == 0), strides in elements.
+ *   scales        [E, N, K/32] uint8 e8m0 (MXFP4, K % 32 == 0), strides in elements.
+ *   expert_ids    [G] int32: expert of group g.
+ *   out           [T, ldo] bf16.
+ * Offsets into B are formed in 64-bit arithmetic (stacks above 2^31 bytes,
+ * reference kernel/nf4_grouped.py:396-399).
+ *
+ * Path selection (forward):
+ *   n_mtiles == 0 -> decode path: every group holds <= 16 rows (the caller
+ *                    guarantees it); `row_off` [G + 1] int32 is required and
+ *                    the tile table is ignored.
+ *   n_mtiles  > 0 -> tiled path: the tile table t_row0/t_rows/t_group
+ *                    [n_mtiles] int32 (reference build_group_tiles,
+ *                    kernel/nf4_grouped.py:334-362) with block_m in
+ *                    {16, 32, 64, 128}; t_rows[i] <= block_m.
+ *
+ * Return codes (the reference CPU tier's convention, gnf4_native/cpu_kernels.c:745-761):
+ *   0 success, -1 shape or argument violation, -2 launch error.
+ */
+#ifndef GNF4_HIP_H_
+#define GNF4_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GNF4_HIP_ABI_VERSION 1
+
+#define GNF4_FMT_NF4 0
+#define GNF4_FMT_MXFP4 1
+
+#define GNF4_DTYPE_BF16 0
+#define GNF4_DTYPE_F16 1
+
+/* ABI version of the loaded library (GNF4_HIP_ABI_VERSION). */
+int gnf4_hip_abi_version(void);
+
+/* Compute units of the current device (0 on error). Replaces the reference's
+ * torch-side SM query `_sm_count` (kernel/nf4_grouped.py:581-591). */
+int gnf4_hip_device_cus(void);
+
+/* Grouped forward for either format: out[t, :] = a[t, :] . dequant(W[e(t)])^T,
+ * fp32 accumulation, one bf16 rounding per output. Replaces the launches in
+ * gemm_4bit_grouped (reference kernel/nf4_grouped.py:750-906: the
+ * _gemv_nf4_grouped / _gemv_nf4_grouped_splitk / _gemm_nf4_grouped grids) and
+ * gemm_mxfp4_grouped (kernel/mxfp4_grouped.py:146-171). */
+int gnf4_hip_grouped_fwd(int fmt, const void *a, int a_dtype, int64_t lda,
+                         const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                         const void *scales, int64_t stride_se, int64_t stride_sn,
+                         const int32_t *expert_ids, const int32_t *row_off, int G,
+                         const int32_t *t_row0, const int32_t *t_rows,
+                         const int32_t *t_group, int n_mtiles, int block_m,
+                         int64_t N, int64_t K, void *out, int64_t ldo, void *stream);
+
+/* NF4 forward (absmax fp32, block 64). Replaces the NF4 kernel launches of
+ * gemm_4bit_grouped, reference kernel/nf4_grouped.py:750-906. */
+int gnf4_hip_nf4_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *B,
+                     int64_t stride_be, int64_t stride_bn, const float *absmax,
+                     int64_t stride_ae, int64_t stride_an, const int32_t *expert_ids,
+                     const int32_t *row_off, int G, const int32_t *t_row0,
+                     const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
+                     int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                     void *stream);
+
+/* MXFP4 forward (e2m1 nibbles, e8m0 scale per 32). Replaces the launches of
+ * gemm_mxfp4_grouped, reference kernel/mxfp4_grouped.py:146-171. */
+int gnf4_hip_mxfp4_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *blocks,
+                       int64_t stride_be, int64_t stride_bn, const uint8_t *scales,
+                       int64_t stride_se, int64_t stride_sn, const int32_t *expert_ids,
+                       const int32_t *row_off, int G, const int32_t *t_row0,
+                       const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
+                       int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                       void *stream);
+
+/* Grouped dgrad for either format: out[t, :] = grad_out[t, :] . dequant(W[e(t)]),
+ * contracting over N in fixed 64-wide ascending steps (output bits do not
+ * depend on block_m). grad_out is [T, ldg] bf16, out is [T, ldo] bf16 with
+ * ldo >= K. Tile table as for the forward tiled path (n_mtiles may be 0:
+ * nothing to do). */
+int gnf4_hip_grouped_dgrad(int fmt, const void *grad_out, int g_dtype, int64_t ldg,
+                           const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                           const void *scales, int64_t stride_se, int64_t stride_sn,
+                           const int32_t *expert_ids, const int32_t *t_row0,
+                           const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
+                           int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                           void *stream);
+
+/* NF4 dgrad. Replaces the _dgrad_nf4_grouped launch of dgrad_4bit_grouped,
+ * reference kernel/nf4_grouped.py:1100-1120. */
+int gnf4_hip_nf4_dgrad(const void *grad_out, int g_dtype, int64_t ldg, const uint8_t *B,
+                       int64_t stride_be, int64_t stride_bn, const float *absmax,
+                       int64_t stride_ae, int64_t stride_an, const int32_t *expert_ids,
+                       const int32_t *t_row0, const int32_t *t_rows,
+                       const int32_t *t_group, int n_mtiles, int block_m, int64_t N,
+                       int64_t K, void *out, int64_t ldo, void *stream);
+
+/* MXFP4 dgrad. The reference has no GPU kernel for it (its backward is a
+ * per-expert Python loop, kernel/mxfp4_qlora.py:106-122); the CPU spec it
+ * follows is gnf4_dgrad_mxfp4_grouped, gnf4_native/cpu_kernels.c:1386-1397. */
+int gnf4_hip_mxfp4_dgrad(const void *grad_out, int g_dtype, int64_t ldg,
+                         const uint8_t *blocks, int64_t stride_be, int64_t stride_bn,
+                         const uint8_t *scales, int64_t stride_se, int64_t stride_sn,
+                         const int32_t *expert_ids, const int32_t *t_row0,
+                         const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
+                         int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GNF4_HIP_H_ */

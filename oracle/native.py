@@ -1,0 +1,174 @@
+"""ctypes bindings to the C oracle and to the compiled reference.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+* ``liboracle.so``      -- ``gnf4_oracle.c`` in this directory (built by
+  ``make -C oracle``); restates the reference's locked tree.
+* ``_ref/libgnf4_ref_v{3,4}.so`` -- the reference's gnf4_native/cpu_kernels.c
+  compiled from its own source by ``oracle/Makefile``; used as an independent
+  check of the restatement and as the timed CPU baseline. The v4 build needs
+  AVX-512; the loader picks the highest level the running CPU supports.
+
+The reference entry points keep its ABI (reference gnf4_native/build.py:103-147):
+``gnf4_gemv_{nf4,mxfp4}_grouped`` and ``gnf4_dgrad_{nf4,mxfp4}_grouped`` take
+(a, B, scales, eids i64[G], sizes i32[G], G, N i64, K i64, out, threads) and
+reject G > 512 or a size < 1.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+FMT = {"nf4": 0, "mxfp4": 1}
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+
+
+def _ptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _cpu_has_avx512() -> bool:
+    try:
+        flags = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        return False
+    return all(f in flags for f in ("avx512f", "avx512bw", "avx512dq", "avx512vl", "avx512cd"))
+
+
+_lib = None
+_ref = None
+_ref_path = None
+
+
+def oracle_lib():
+    """The C oracle; raises with a build hint if it was not built."""
+    global _lib
+    if _lib is None:
+        path = HERE / "liboracle.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        lib = ctypes.CDLL(str(path))
+        for name in ("gnf4o_gemv_grouped", "gnf4o_dgrad_grouped"):
+            fn = getattr(lib, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.c_int, _P, _P, _P, _P, _P, ctypes.c_int,
+                           _I64, _I64, _I64, _P, ctypes.c_int]
+        lib.gnf4o_nf4_lut.restype = ctypes.POINTER(ctypes.c_float)
+        lib.gnf4o_fp4_lut.restype = ctypes.POINTER(ctypes.c_float)
+        _lib = lib
+    return _lib
+
+
+def ref_lib():
+    """The compiled reference (or None when it was not built here)."""
+    global _ref, _ref_path
+    if _ref is None:
+        cands = []
+        if _cpu_has_avx512():
+            cands.append(HERE / "_ref" / "libgnf4_ref_v4.so")
+        cands.append(HERE / "_ref" / "libgnf4_ref_v3.so")
+        for path in cands:
+            if path.exists():
+                lib = ctypes.CDLL(str(path))
+                for name in ("gnf4_gemv_nf4_grouped", "gnf4_gemv_mxfp4_grouped",
+                             "gnf4_dgrad_nf4_grouped", "gnf4_dgrad_mxfp4_grouped"):
+                    fn = getattr(lib, name)
+                    fn.restype = ctypes.c_int
+                    fn.argtypes = [_P, _P, _P, _P, _P, ctypes.c_int, _I64, _I64,
+                                   _P, ctypes.c_int]
+                _ref, _ref_path = lib, path
+                break
+    return _ref
+
+
+def ref_path():
+    ref_lib()
+    return _ref_path
+
+
+def _prep(a, packed, scales, sizes, expert_ids, fmt):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    scales = np.ascontiguousarray(
+        scales, dtype=np.float32 if fmt == "nf4" else np.uint8)
+    eids = np.ascontiguousarray(np.asarray(expert_ids, dtype=np.int64))
+    sz = np.ascontiguousarray(np.asarray(sizes, dtype=np.int32))
+    return a, packed, scales, eids, sz
+
+
+def gemv_grouped(a, packed, scales, sizes, expert_ids, *, fmt, threads=0):
+    """Oracle forward (fp32 [R, N]), locked tree."""
+    a, packed, scales, eids, sz = _prep(a, packed, scales, sizes, expert_ids, fmt)
+    E, N, half = packed.shape
+    out = np.empty((a.shape[0], N), dtype=np.float32)
+    rc = oracle_lib().gnf4o_gemv_grouped(
+        FMT[fmt], _ptr(a), _ptr(packed), _ptr(scales), _ptr(eids), _ptr(sz),
+        len(sz), E, N, half * 2, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"gnf4o_gemv_grouped rejected the call (rc={rc})")
+    return out
+
+
+def dgrad_grouped(g, packed, scales, sizes, expert_ids, *, fmt, threads=0):
+    """Oracle dgrad (fp32 [R, K]), ascending-n chain."""
+    g, packed, scales, eids, sz = _prep(g, packed, scales, sizes, expert_ids, fmt)
+    E, N, half = packed.shape
+    out = np.zeros((g.shape[0], half * 2), dtype=np.float32)
+    rc = oracle_lib().gnf4o_dgrad_grouped(
+        FMT[fmt], _ptr(g), _ptr(packed), _ptr(scales), _ptr(eids), _ptr(sz),
+        len(sz), E, N, half * 2, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"gnf4o_dgrad_grouped rejected the call (rc={rc})")
+    return out
+
+
+def ref_gemv_grouped(a, packed, scales, sizes, expert_ids, *, fmt, threads=0):
+    """The compiled reference's forward (sizes must be >= 1, G <= 512)."""
+    lib = ref_lib()
+    if lib is None:
+        raise RuntimeError("reference build absent (oracle/_ref)")
+    a, packed, scales, eids, sz = _prep(a, packed, scales, sizes, expert_ids, fmt)
+    E, N, half = packed.shape
+    out = np.empty((a.shape[0], N), dtype=np.float32)
+    fn = lib.gnf4_gemv_nf4_grouped if fmt == "nf4" else lib.gnf4_gemv_mxfp4_grouped
+    rc = fn(_ptr(a), _ptr(packed), _ptr(scales), _ptr(eids), _ptr(sz), len(sz),
+            N, half * 2, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"reference gemv rejected the call (rc={rc})")
+    return out
+
+
+def ref_dgrad_grouped(g, packed, scales, sizes, expert_ids, *, fmt, threads=0):
+    """The compiled reference's dgrad (caller-zeroed output)."""
+    lib = ref_lib()
+    if lib is None:
+        raise RuntimeError("reference build absent (oracle/_ref)")
+    g, packed, scales, eids, sz = _prep(g, packed, scales, sizes, expert_ids, fmt)
+    E, N, half = packed.shape
+    out = np.zeros((g.shape[0], half * 2), dtype=np.float32)
+    fn = lib.gnf4_dgrad_nf4_grouped if fmt == "nf4" else lib.gnf4_dgrad_mxfp4_grouped
+    rc = fn(_ptr(g), _ptr(packed), _ptr(scales), _ptr(eids), _ptr(sz), len(sz),
+            N, half * 2, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"reference dgrad rejected the call (rc={rc})")
+    return out
+
+
+def oracle_luts():
+    lib = oracle_lib()
+    nf4 = np.ctypeslib.as_array(lib.gnf4o_nf4_lut(), shape=(16,)).copy()
+    fp4 = np.ctypeslib.as_array(lib.gnf4o_fp4_lut(), shape=(16,)).copy()
+    return nf4, fp4
+
+
+def build() -> None:
+    """Compile the oracle (and the reference when its source is present)."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True,
+                   env=dict(os.environ))

@@ -1,0 +1,294 @@
+"""GPU parity of the forward ops against the oracle and the tolerance contract.
+
+Bars (reference docs/TOLERANCE_CONTRACT.md, kernel/test_nf4_grouped.py):
+  * decode/unpack: bit-exact. One-hot activations make each output a single
+    decoded weight, so out == dequant(W).to(bf16) exactly, for every code in
+    both nibble positions, on both kernels (decode and tiled).
+  * full outputs: B-abs rel-Frobenius <= 1e-2 vs fp64 and B-rel <= 2x the bf16
+    dequant-then-matmul path; agreement with the C oracle (the reference's
+    locked CPU tree) within 1e-2 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _fixtures import (contract_check, dequant, oracle_fwd, rand_acts, rand_mx_stack,
+                       rand_nf4_stack, rel_err, spread_ids)
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from mxfp4_grouped import gemm_mxfp4_grouped
+    from nf4_grouped import gemm_4bit_grouped
+    return {"nf4": gemm_4bit_grouped, "mxfp4": gemm_mxfp4_grouped}
+
+
+def _stack(fmt, E, N, K, seed=0):
+    return rand_nf4_stack(E, N, K, seed) if fmt == "nf4" else rand_mx_stack(E, N, K, seed)
+
+
+def test_native_library_is_the_one_in_tree():
+    import _hiplib
+    lib = _hiplib.load()
+    assert lib.gnf4_hip_abi_version() == _hiplib.ABI_VERSION
+    assert lib.gnf4_hip_device_cus() > 0
+    assert str(_hiplib.LIB_PATH).endswith("grouped-nf4-gemm_amd/libgnf4_hip.so")
+
+
+# ------------------------------------------------------------ exactness --
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_all_codes_both_nibble_positions_tiled(fmt):
+    """Every (code, position) pair via one-hot rows (reference
+    kernel/test_nf4_grouped.py:92-109): K one-hot rows -> tiled kernel."""
+    N, K = 16, 64
+    B = torch.empty(1, N, K // 2, dtype=torch.uint8, device="cuda")
+    for c in range(16):
+        B[0, c, :] = (c << 4) | (15 - c)
+    if fmt == "nf4":
+        S = torch.ones(1, N, K // 64, dtype=torch.float32, device="cuda")
+    else:
+        S = torch.full((1, N, K // 32), 127, dtype=torch.uint8, device="cuda")
+    eye = torch.eye(K, dtype=torch.bfloat16, device="cuda")
+    out = _ops()[fmt](eye, B, S, [K], [0])
+    ref = dequant(fmt, B[0], S[0])
+    assert torch.equal(out.t(), ref.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_every_byte_every_position_with_scales(fmt):
+    """All 256 byte values in every row, random per-block scales: the one-hot
+    product through the tiled kernel equals the bf16-rounded decode."""
+    N, K = 48, 512
+    g = torch.Generator().manual_seed(5)
+    perm = torch.stack([torch.randperm(256, generator=g) for _ in range(N)]).to(torch.uint8)
+    B = perm.reshape(1, N, 256).cuda()
+    if fmt == "nf4":
+        S = (torch.rand(1, N, K // 64, generator=g) * 4 + 0.01).cuda()
+    else:
+        S = torch.randint(100, 150, (1, N, K // 32), generator=g, dtype=torch.uint8).cuda()
+    eye = torch.eye(K, dtype=torch.bfloat16, device="cuda")
+    out = _ops()[fmt](eye, B, S, [K], [0])
+    ref = dequant(fmt, B[0], S[0]).to(torch.bfloat16)
+    assert torch.equal(out.t(), ref)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("k_hot", [0, 100, 511])
+def test_decode_kernel_one_hot_exact(fmt, k_hot):
+    """Decode kernel (M = 1): a one-hot row selects one weight column exactly
+    (reference kernel/test_nf4_grouped.py:257-265)."""
+    N, K = 144, 512
+    B, S = _stack(fmt, 3, N, K, seed=7)
+    a = torch.zeros(1, K, dtype=torch.bfloat16, device="cuda")
+    a[0, k_hot] = 1.0
+    out = _ops()[fmt](a, B, S, [1], [2])
+    ref = dequant(fmt, B[2], S[2])[:, k_hot].to(torch.bfloat16)
+    assert torch.equal(out[0], ref)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_decode_kernel_sixteen_one_hot_rows(fmt):
+    """A 16-row group through the decode kernel: row r one-hot at k = 37 r."""
+    N, K = 64, 640
+    B, S = _stack(fmt, 2, N, K, seed=9)
+    a = torch.zeros(16, K, dtype=torch.bfloat16, device="cuda")
+    for r in range(16):
+        a[r, 37 * r] = 1.0
+    out = _ops()[fmt](a, B, S, [16], [1])
+    w = dequant(fmt, B[1], S[1]).to(torch.bfloat16)
+    for r in range(16):
+        assert torch.equal(out[r], w[:, 37 * r]), r
+
+
+# ------------------------------------------------------------- tolerance --
+
+SHAPES = [  # (name, fmt, N, K, E, k)
+    ("c1_tiny", "nf4", 512, 1024, 8, 8),
+    ("qwen_gu", "nf4", 1536, 2048, 128, 8),
+    ("qwen_dn", "nf4", 2048, 768, 128, 8),
+    ("gptoss_gu", "mxfp4", 5760, 2880, 32, 4),
+    ("gptoss_dn", "mxfp4", 2880, 2880, 32, 4),
+]
+
+
+@pytest.mark.parametrize("name,fmt,N,K,E,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 4, 16, 128, 290])
+def test_contract_census_shapes(name, fmt, N, K, E, k, m):
+    active = spread_ids(E, k)
+    Wa, Sa = _stack(fmt, len(active), N, K, seed=11)
+    # place the active experts at their ids inside a zero stack view-free:
+    # use a stack of E experts where only the active ids are populated
+    W = torch.zeros(E, N, K // 2, dtype=torch.uint8, device="cuda")
+    S = torch.zeros((E, N, K // (64 if fmt == "nf4" else 32)), dtype=Sa.dtype, device="cuda")
+    W[active] = Wa
+    S[active] = Sa
+    sizes = [m] * len(active)
+    a = rand_acts(sum(sizes), K, seed=12)
+    out = _ops()[fmt](a, W, S, sizes, active)
+    e_f, e_d = contract_check(fmt, out, a, W, S, sizes, active)
+    print(f"PFID {name} m={m}: fused {e_f:.3e} dequant {e_d:.3e} ratio {e_f / e_d:.2f}")
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("sizes,ids", [([1] * 8, list(range(8))),
+                                       ([4, 1, 2, 3], [7, 0, 3, 5]),
+                                       ([33, 2, 70], [1, 6, 4])])
+def test_agrees_with_the_c_oracle(fmt, sizes, ids):
+    """The GPU output against the reference's locked CPU tree (restated in
+    oracle/gnf4_oracle.c, bit-exact to the compiled reference)."""
+    N, K = 512, 1024
+    W, S = _stack(fmt, 8, N, K, seed=3)
+    a = rand_acts(sum(sizes), K, seed=4)
+    out = _ops()[fmt](a, W, S, sizes, ids)
+    ref = torch.from_numpy(oracle_fwd(fmt, a, W, S, sizes, ids))
+    assert rel_err(out.float().cpu(), ref) < 1e-2
+
+
+# ------------------------------------------------------------ boundaries --
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_single_token_groups(fmt):
+    W, S = _stack(fmt, 8, 128, 128)
+    a = rand_acts(3, 128)
+    out = _ops()[fmt](a, W, S, [1, 1, 1], [2, 5, 7])
+    assert out.shape == (3, 128)
+    contract_check(fmt, out, a, W, S, [1, 1, 1], [2, 5, 7])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_all_tokens_one_expert(fmt):
+    W, S = _stack(fmt, 8, 128, 128)
+    a = rand_acts(200, 128)
+    out = _ops()[fmt](a, W, S, [200], [3])
+    contract_check(fmt, out, a, W, S, [200], [3])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_noncontiguous_unsorted_ids(fmt):
+    W, S = _stack(fmt, 8, 128, 128)
+    a = rand_acts(30, 128)
+    sizes, ids = [10, 5, 15], [6, 1, 4]
+    out = _ops()[fmt](a, W, S, sizes, ids)
+    contract_check(fmt, out, a, W, S, sizes, ids)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_k_equals_blocksize(fmt, m):
+    K = 64 if fmt == "nf4" else 32
+    W, S = _stack(fmt, 2, 64, K)
+    a = rand_acts(m, K)
+    out = _ops()[fmt](a, W, S, [m], [1])
+    contract_check(fmt, out, a, W, S, [m], [1])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_ragged_tail_tiles_and_n_tail(fmt):
+    W, S = _stack(fmt, 8, 200, 192)
+    a = rand_acts(65 + 17, 192)
+    out = _ops()[fmt](a, W, S, [65, 17], [0, 7], block_m=64)
+    contract_check(fmt, out, a, W, S, [65, 17], [0, 7])
+
+
+@pytest.mark.parametrize("K", [32, 96, 160, 2880])
+def test_mxfp4_k_not_a_multiple_of_64(K):
+    W, S = rand_mx_stack(3, 96, K)
+    for sizes in ([1, 1], [3, 9], [20, 50]):
+        a = rand_acts(sum(sizes), K)
+        out = _ops()["mxfp4"](a, W, S, sizes, [2, 0])
+        contract_check("mxfp4", out, a, W, S, sizes, [2, 0])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_expert_id_forms_bitwise_equal_with_empty_group(fmt):
+    """list / CPU tensor / device tensor ids give identical bits, including a
+    zero-size group (reference kernel/test_eids_forms.py:27, :66-92)."""
+    W, S = _stack(fmt, 6, 256, 256)
+    sizes = [3, 1, 0, 5, 2]
+    ids = [4, 0, 2, 5, 1]
+    a = rand_acts(sum(sizes), 256)
+    op = _ops()[fmt]
+    for bm in (None, 16):
+        base = op(a, W, S, sizes, ids, block_m=bm)
+        cpu_t = op(a, W, S, sizes, torch.tensor(ids, dtype=torch.int32), block_m=bm)
+        dev_t = op(a, W, S, sizes, torch.tensor(ids, dtype=torch.int64, device="cuda"), block_m=bm)
+        assert torch.equal(base, cpu_t) and torch.equal(base, dev_t)
+        keep = [i for i, m in enumerate(sizes) if m]
+        contract_check(fmt, base, a, W, S, [sizes[i] for i in keep], [ids[i] for i in keep])
+
+
+def test_sizes_tensor_is_not_mutated():
+    from nf4_grouped import gemm_4bit_grouped
+    W, S = rand_nf4_stack(4, 128, 128)
+    sizes = torch.tensor([40, 0, 25])
+    a = rand_acts(65, 128)
+    gemm_4bit_grouped(a, W, S, sizes, [0, 1, 2])
+    out2 = gemm_4bit_grouped(a, W, S, sizes, [0, 1, 2])
+    assert sizes.tolist() == [40, 0, 25]
+    assert out2.shape == (65, 128)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_repeat_runs_bitwise_identical(fmt):
+    """Determinism: same inputs, same bits (no atomics in any reduction)."""
+    W, S = _stack(fmt, 16, 768, 1024)
+    for sizes in ([1] * 12, [3, 16, 2, 9], [130, 7, 64]):
+        ids = list(range(len(sizes)))
+        a = rand_acts(sum(sizes), 1024)
+        x = _ops()[fmt](a, W, S, sizes, ids)
+        y = _ops()[fmt](a, W, S, sizes, ids)
+        assert torch.equal(x, y)
+
+
+def test_split_k_and_tuning_knobs_keep_the_result():
+    """The reference's schedule knobs are accepted and leave the bits alone."""
+    from nf4_grouped import gemm_4bit_grouped
+    W, S = rand_nf4_stack(8, 512, 2048)
+    a = rand_acts(2, 2048)
+    one = gemm_4bit_grouped(a, W, S, [1, 1], [0, 4], split_k=1)
+    for sk in (2, 4, 8):
+        assert torch.equal(gemm_4bit_grouped(a, W, S, [1, 1], [0, 4], split_k=sk), one)
+    assert torch.equal(gemm_4bit_grouped(a, W, S, [1, 1], [0, 4], decode_config=(128, 4)), one)
+    a2 = rand_acts(256, 2048)
+    base = gemm_4bit_grouped(a2, W, S, [128, 128], [1, 5])
+    for kw in (dict(prefill_config=(64, 4, 3)), dict(prefill_variant=0),
+               dict(prefill_variant=3), dict(prefill_groups=2)):
+        assert torch.equal(gemm_4bit_grouped(a2, W, S, [128, 128], [1, 5], **kw), base)
+    with pytest.raises(ValueError, match="prefill_variant"):
+        gemm_4bit_grouped(a2, W, S, [128, 128], [1, 5], prefill_variant=2)
+
+
+def test_stack_beyond_2gib_offsets():
+    """Experts on both sides of a 2^31-byte stack (reference
+    kernel/test_offsets_2gib.py:79-110): 64-bit offset arithmetic."""
+    from nf4_grouped import gemm_4bit_grouped
+    E, N, K = 257, 4096, 4096          # 8 MiB per expert -> 2.01 GiB stack
+    W = torch.randint(0, 256, (E, N, K // 2), dtype=torch.uint8, device="cuda")
+    S = torch.rand(E, N, K // 64, device="cuda") * 0.05 + 0.01
+    assert W.numel() > 2 ** 31
+    ids = [0, 128, 256]
+    for m in (1, 40):
+        a = rand_acts(3 * m, K)
+        out = gemm_4bit_grouped(a, W, S, [m] * 3, ids)
+        contract_check("nf4", out, a, W, S, [m] * 3, ids)
+    del W
+
+
+def test_mxfp4_e8m0_edges_follow_exp2_multiply():
+    """0xFF decodes as 2^128 (inf for nonzero codes, NaN for zero codes);
+    0x00 as 2^-127. The one-hot path shows the decoded value directly."""
+    from mxfp4_grouped import gemm_mxfp4_grouped
+    N, K = 16, 64
+    B = torch.empty(1, N, K // 2, dtype=torch.uint8, device="cuda")
+    B[0, :, :] = 0x21                    # elements (0.5, 1.0) pairwise
+    S = torch.full((1, N, K // 32), 127, dtype=torch.uint8, device="cuda")
+    S[0, 1, :] = 0                        # subnormal scale 2^-127
+    S[0, 2, :] = 130
+    a = torch.zeros(1, K, dtype=torch.bfloat16, device="cuda")
+    a[0, 1] = 1.0                         # element 1 = high nibble of byte 0 = 1.0
+    out = gemm_mxfp4_grouped(a, B, S, [1], [0]).float()
+    assert out[0, 0].item() == 1.0
+    assert out[0, 2].item() == 8.0
+    assert out[0, 1].item() in (2.0 ** -127, 0.0)   # subnormal kept or flushed

@@ -1,0 +1,401 @@
+"""Benchmark: grouped 4-bit MoE expert GEMM on one MI355X.
+
+Headline workload: Qwen3-30B-A3B expert shapes,
+NF4 decode. One step = the expert GEMMs of one decode token through all 48
+MoE layers: per layer gate_up [128 experts, 1536, 2048] and down [128, 2048,
+768], top-8 uniformly routed experts, M = 1 row per active expert. Each layer
+has its own packed weights (48 x 302 MB = 14.5 GB resident in HBM), so the
+step's 906 MB of packed bytes come from HBM, not the 256 MB Infinity Cache.
+The step is captured once as a HIP graph and replayed.
+
+metric value = packed weight bytes of the active experts / step time (GB/s).
+
+Also reported:
+  roofline     the dominant kernel (NF4 decode, gate_up) timed per launch
+               with HIP events on its stream, against the 8 TB/s HBM peak.
+  cpu_baseline the reference's own CPU kernels (gnf4_native/cpu_kernels.c
+               compiled by oracle/Makefile) on the host cores, same shapes.
+  extra        batch 4 / 16 decode, GPT-OSS-20B MXFP4 decode, Qwen3 NF4
+               Zipf prefill and down-projection dgrad TFLOP/s.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "grouped-nf4-gemm_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+
+QWEN = dict(E=128, gu=(1536, 2048), dn=(2048, 768), top_k=8, layers=48)
+GPTOSS = dict(E=32, gu=(5760, 2880), dn=(2880, 2880), top_k=4, layers=24)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def route(rng, tokens, top_k, E, zipf_s=None):
+    import numpy as np
+    counts = np.zeros(E, dtype=np.int64)
+    if zipf_s is None:
+        for _ in range(tokens):
+            counts[rng.choice(E, size=top_k, replace=False)] += 1
+    else:
+        p = 1.0 / np.arange(1, E + 1) ** zipf_s
+        p = p[rng.permutation(E)]
+        p /= p.sum()
+        for _ in range(tokens):
+            counts[rng.choice(E, size=top_k, replace=False, p=p)] += 1
+    ids = [int(e) for e in np.nonzero(counts)[0]]
+    return [int(counts[e]) for e in ids], ids
+
+
+def make_nf4_layers(E, N, K, layers, dev, seed):
+    """One genuinely quantized N(0, 0.02) NF4 layer, cloned per layer."""
+    import torch
+    from nf4_pack_ref import quantize_pack_nf4
+    g = torch.Generator(device=dev).manual_seed(seed)
+    W = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
+    A = torch.empty(E, N, K // 64, dtype=torch.float32, device=dev)
+    for e in range(E):
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        W[e], A[e] = quantize_pack_nf4(w)
+    out = [(W, A)]
+    for _ in range(layers - 1):
+        out.append((W.clone(), A.clone()))
+    return out
+
+
+def make_mx_layers(E, N, K, layers, dev, seed):
+    import torch
+    from mxfp4_pack_ref import quantize_pack_mxfp4
+    g = torch.Generator(device=dev).manual_seed(seed)
+    W = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
+    S = torch.empty(E, N, K // 32, dtype=torch.uint8, device=dev)
+    for e in range(E):
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        b, s = quantize_pack_mxfp4(w)
+        W[e], S[e] = b.reshape(N, K // 2), s
+    out = [(W, S)]
+    for _ in range(layers - 1):
+        out.append((W.clone(), S.clone()))
+    return out
+
+
+class DecodeModel:
+    """Expert GEMMs of a decode step through every MoE layer."""
+
+    def __init__(self, fmt, cfg, batch, dev, seed=0, layers=None):
+        import numpy as np
+        import torch
+        self.fmt, self.cfg, self.batch, self.dev = fmt, cfg, batch, dev
+        L = layers or cfg["layers"]
+        E = cfg["E"]
+        mk = make_nf4_layers if fmt == "nf4" else make_mx_layers
+        self.gu = mk(E, *cfg["gu"], L, dev, seed)
+        self.dn = mk(E, *cfg["dn"], L, dev, seed + 1)
+        rng = np.random.default_rng(seed + 7)
+        self.routes = []
+        g = torch.Generator(device=dev).manual_seed(seed + 3)
+        for _ in range(L):
+            sizes, ids = route(rng, batch, cfg["top_k"], E)
+            T = sum(sizes)
+            x = torch.randn(T, cfg["gu"][1], generator=g, device=dev).to(torch.bfloat16)
+            h = torch.randn(T, cfg["dn"][1], generator=g, device=dev).to(torch.bfloat16)
+            eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+            self.routes.append((sizes, eids, x, h))
+        N1, K1 = cfg["gu"]
+        N2, K2 = cfg["dn"]
+        self.bytes_gu = [len(r[0]) * N1 * K1 // 2 for r in self.routes]
+        self.bytes_dn = [len(r[0]) * N2 * K2 // 2 for r in self.routes]
+        self.packed_bytes = sum(self.bytes_gu) + sum(self.bytes_dn)
+        self.L = L
+
+    def op(self):
+        if self.fmt == "nf4":
+            from nf4_grouped import gemm_4bit_grouped
+            return gemm_4bit_grouped
+        from mxfp4_grouped import gemm_mxfp4_grouped
+        return gemm_mxfp4_grouped
+
+    def step(self):
+        op = self.op()
+        outs = []
+        for l in range(self.L):
+            sizes, eids, x, h = self.routes[l]
+            outs.append(op(x, *self.gu[l], sizes, eids))
+            outs.append(op(h, *self.dn[l], sizes, eids))
+        return outs
+
+    def kernel_durations(self, which="gu", reps=3):
+        """Per-launch durations (ms) of one projection across all layers, from
+        HIP events recorded on the launch stream around each kernel. A sleep
+        kernel queued first keeps the GPU busy while the host enqueues, so
+        each event pair brackets only its kernel."""
+        import torch
+        op = self.op()
+        stream = torch.cuda.current_stream(self.dev)
+        durs = []
+        for _ in range(reps):
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(self.L + 1)]
+            torch.cuda._sleep(int(2.4e9 * 0.004))          # ~4 ms of queue cover
+            for l in range(self.L):
+                sizes, eids, x, h = self.routes[l]
+                evs[l].record(stream)
+                if which == "gu":
+                    op(x, *self.gu[l], sizes, eids)
+                else:
+                    op(h, *self.dn[l], sizes, eids)
+            evs[self.L].record(stream)
+            torch.cuda.synchronize()
+            durs += [evs[l].elapsed_time(evs[l + 1]) for l in range(self.L)]
+        return durs
+
+
+def time_graph(fn, steps, warmup, dev):
+    """Capture fn() as a graph, then time `steps` replays after `warmup`."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps, graph
+
+
+def cpu_baseline(model, budget_s=10.0, layers=4):
+    """The reference's CPU kernels on the host cores over a bounded sample:
+    `layers` layers of the same decode workload (gate_up + down per layer),
+    repeated until ~budget_s of CPU time. fp32 activations are converted
+    once, outside the timed region (as the reference's CPU tier does)."""
+    import numpy as np
+    from oracle import native
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    ref = native.ref_lib()
+    kind = "reference" if ref is not None else "port"
+    fwd = native.ref_gemv_grouped if ref is not None else native.gemv_grouped
+    L = min(layers, model.L)
+    host = []
+    for l in range(L):
+        sizes, eids, x, h = model.routes[l]
+        ids = eids.cpu().tolist()
+        host.append((sizes, ids, x.float().cpu().numpy(), h.float().cpu().numpy(),
+                     model.gu[l][0].cpu().numpy(), model.gu[l][1].cpu().numpy(),
+                     model.dn[l][0].cpu().numpy(), model.dn[l][1].cpu().numpy()))
+    nbytes = sum(model.bytes_gu[:L]) + sum(model.bytes_dn[:L])
+    fmt = model.fmt
+
+    def one_pass():
+        for sizes, ids, x, h, gw, gs, dw, ds in host:
+            fwd(x, gw, gs, sizes, ids, fmt=fmt, threads=threads)
+            fwd(h, dw, ds, sizes, ids, fmt=fmt, threads=threads)
+
+    one_pass()                                       # warm the pages
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one_pass()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    gbs = nbytes * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{reps} passes x {L} layers (gate_up+down, batch {model.batch}, "
+                      f"top-{model.cfg['top_k']}) in {el:.1f} s; "
+                      f"{'oracle/_ref ' + native.ref_path().name if ref is not None else 'oracle/liboracle.so'}",
+            "ms_per_layer_pass": round(el * 1e3 / reps / L, 3)}
+
+
+def prefill_tflops(dev, seed=0):
+    """Config 4: Qwen3 NF4 prefill, 4096 tokens x top-8 Zipf(1.1) routing."""
+    import numpy as np
+    import torch
+    from nf4_grouped import gemm_4bit_grouped
+    (W, A), = make_nf4_layers(128, 1536, 2048, 1, dev, seed)
+    (W2, A2), = make_nf4_layers(128, 2048, 768, 1, dev, seed + 1)
+    sizes, ids = route(np.random.default_rng(seed), 4096, 8, 128, zipf_s=1.1)
+    T = sum(sizes)
+    x = torch.randn(T, 2048, device=dev).to(torch.bfloat16)
+    h = torch.randn(T, 768, device=dev).to(torch.bfloat16)
+    eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+    res = {}
+    for name, a, Wt, At, N, K in (("gate_up", x, W, A, 1536, 2048), ("down", h, W2, A2, 2048, 768)):
+        for _ in range(3):
+            gemm_4bit_grouped(a, Wt, At, sizes, eids)
+        torch.cuda.synchronize()
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        reps = 10
+        evs[0].record()
+        for _ in range(reps):
+            gemm_4bit_grouped(a, Wt, At, sizes, eids)
+        evs[1].record()
+        torch.cuda.synchronize()
+        ms = evs[0].elapsed_time(evs[1]) / reps
+        tf = 2.0 * T * N * K / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    res["rows"] = T
+    res["m_min_max"] = [min(sizes), max(sizes)]
+    return res
+
+
+def dgrad_tflops(dev, seed=0):
+    """Config 5: NF4 dgrad on the Qwen3 down projection, 2048 tokens x top-8."""
+    import numpy as np
+    import torch
+    from nf4_grouped import dgrad_4bit_grouped
+    (W, A), = make_nf4_layers(128, 2048, 768, 1, dev, seed)
+    sizes, ids = route(np.random.default_rng(seed + 1), 2048, 8, 128)
+    T = sum(sizes)
+    go = (torch.randn(T, 2048, device=dev) * 1e-2).to(torch.bfloat16)
+    eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        dgrad_4bit_grouped(go, W, A, sizes, eids)
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    reps = 10
+    evs[0].record()
+    for _ in range(reps):
+        dgrad_4bit_grouped(go, W, A, sizes, eids)
+    evs[1].record()
+    torch.cuda.synchronize()
+    ms = evs[0].elapsed_time(evs[1]) / reps
+    tf = 2.0 * T * 2048 * 768 / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "tflops": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "rows": T}
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed PMC
+    summary, if present (line `traffic_bytes_per_launch: <int>`)."""
+    p = ROOT / "profiles" / "decode_nf4_qwen3_gate_up_b1_pmc.md"
+    if not p.exists():
+        return None
+    for line in p.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=QWEN["layers"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(expert parallelism is design-only). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    log(f"[bench] building Qwen3-30B-A3B NF4 decode model: {args.layers} layers, batch {args.batch}")
+    model = DecodeModel("nf4", QWEN, args.batch, dev, layers=args.layers)
+    ms, graph = time_graph(model.step, args.steps, args.warmup, dev)
+    value = model.packed_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] step {ms:.4f} ms, {model.packed_bytes / 1e6:.1f} MB packed -> {value:.1f} GB/s")
+
+    durs = model.kernel_durations("gu")
+    avg_ms = sum(durs) / len(durs)
+    per_launch = sum(model.bytes_gu) / len(model.bytes_gu)
+    achieved = per_launch / (avg_ms * 1e-3) / 1e9
+    dn = model.kernel_durations("dn")
+    dn_ms = sum(dn) / len(dn)
+    dn_gbs = (sum(model.bytes_dn) / len(model.bytes_dn)) / (dn_ms * 1e-3) / 1e9
+    log(f"[bench] gate_up decode kernel {avg_ms * 1e3:.2f} us -> {achieved:.1f} GB/s; "
+        f"down {dn_ms * 1e3:.2f} us -> {dn_gbs:.1f} GB/s")
+
+    extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1)}}
+    if not args.no_extra:
+        for b in (4, 16):
+            m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=8)
+            d = m.kernel_durations("gu")
+            a = sum(m.bytes_gu) / len(m.bytes_gu) / (sum(d) / len(d) * 1e-3) / 1e9
+            d2 = m.kernel_durations("dn")
+            a2 = sum(m.bytes_dn) / len(m.bytes_dn) / (sum(d2) / len(d2) * 1e-3) / 1e9
+            extra[f"qwen3_nf4_decode_b{b}"] = {"gate_up_gbs": round(a, 1), "down_gbs": round(a2, 1),
+                                               "experts_per_layer": round(sum(len(r[0]) for r in m.routes) / m.L, 1)}
+            del m
+        for b in (1, 64):
+            m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=6)
+            d = m.kernel_durations("gu")
+            a = sum(m.bytes_gu) / len(m.bytes_gu) / (sum(d) / len(d) * 1e-3) / 1e9
+            d2 = m.kernel_durations("dn")
+            a2 = sum(m.bytes_dn) / len(m.bytes_dn) / (sum(d2) / len(d2) * 1e-3) / 1e9
+            extra[f"gptoss20b_mxfp4_decode_b{b}"] = {"gate_up_gbs": round(a, 1), "down_gbs": round(a2, 1)}
+            del m
+        torch.cuda.empty_cache()
+        extra["qwen3_nf4_prefill_zipf"] = prefill_tflops(dev)
+        extra["qwen3_nf4_dgrad_down"] = dgrad_tflops(dev)
+        log(f"[bench] extra: {json.dumps(extra)}")
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] timing the CPU baseline")
+        cpu = cpu_baseline(model, budget_s=args.cpu_seconds)
+        log(f"[bench] cpu: {cpu}")
+
+    line = {
+        "metric": "packed-weight GB/s at M=1 decode (Qwen3-30B-A3B NF4 experts, all 48 MoE layers)",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) weights NF4-quantized (one layer, cloned per layer), "
+                "N(0,1) bf16 activations, seeded uniform top-8 routing",
+        "config": {"workload": "qwen3-30b-a3b nf4 decode: 48 layers x (gate_up 1536x2048 + down 2048x768), "
+                               f"E=128, top-8, batch {args.batch}, HIP graph replay",
+                   "batch": args.batch, "layers": model.L,
+                   "packed_bytes_per_step": model.packed_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
+                     "kernel": "k_decode_fwd<NF4> (gate_up, 8 experts x 1536 x 1024 B per launch)",
+                     "avg_launch_us": round(avg_ms * 1e3, 3), "launches_timed": len(durs)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -30,7 +30,8 @@
 //                  weight tile straight from HBM through registers, 16 bytes
 //                  per lane per 128-element chunk, with a prefetch ring; the
 //                  group's <= 16 activation rows ride along as the MFMA A
-//                  operand. Persistent grid, units = (group, 16-row n-tile).
+//                  operand. One workgroup per unit (group, 16-row n-tile);
+//                  its four waves split the K chunks and reduce through LDS.
 //   k_gemm_fwd     large groups (prefill). BM x 128 output tiles over ragged
 //                  groups from a host tile table; per 64-wide k-step the
 //                  activation tile and the decoded weight tile are staged in
@@ -71,17 +72,31 @@ __constant__ float c_nf4[16] = {
 
 // ---------------------------------------------------------------- decode --
 
-// The NF4 pair table: 256 bytes x 32 lane columns x float2 = 64 KiB. Declared
-// first so it sits at LDS offset 0 and the perm result is the full address.
+// The NF4 pair table: 256 bytes x 32 lane columns x float2 = 64 KiB. Entry
+// (byte, column) holds the fp32 pair (NF4[byte >> 4], NF4[byte & 15]) in the
+// column of lane % 32, so the lanes one LDS pass serves read distinct banks.
+// Declared first so it sits at LDS offset 0: one v_perm_b32 then forms the
+// full address byte << 8 | (lane % 32) * 8.
 constexpr int kPairEntries = 256 * 32;
 
-__device__ __forceinline__ void init_pair_table(float2* tab) {
-  // thread t fills the 32 columns of byte t, rotating the column order by
-  // lane so one store instruction touches 64 distinct banks.
-  for (int b = threadIdx.x; b < 256; b += blockDim.x) {
-    const float2 v = make_float2(c_nf4[b >> 4], c_nf4[b & 15]);
-    for (int j = 0; j < 32; ++j) tab[b * 32 + ((j + b) & 31)] = v;
-  }
+// Codebook entry `lane % 16` in one register per lane. Kernels load it before
+// any weight load: vector loads complete in order, so a codebook read issued
+// after the weights would hold the table build until every weight landed.
+__device__ __forceinline__ int nf4_lut_lane() {
+  return __float_as_int(c_nf4[threadIdx.x & 15]);
+}
+
+__device__ __forceinline__ void init_pair_table(float2* tab, int lut) {
+  // Thread t (of the 256 every kernel here launches) fills the 32 columns of
+  // byte t, rotating the column order by byte so one store instruction
+  // touches distinct banks. Entries come from the codebook register of lanes
+  // 0..15 through ds_bpermute.
+  const unsigned b = threadIdx.x;
+  const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b >> 4) << 2), lut));
+  const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b & 15) << 2), lut));
+  const float2 e = make_float2(hi, lo);
+#pragma unroll
+  for (int j = 0; j < 32; ++j) tab[b * 32 + ((j + b) & 31)] = e;
 }
 
 __device__ __forceinline__ unsigned bf16x2_bits(float lo, float hi) {
@@ -101,6 +116,24 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16(const float2* tab, unsigned
     r[i] = bf16x2_bits(p.x * s, p.y * s);
   }
   return r;
+}
+
+// 32 NF4 elements (16 packed bytes) -> 4 MFMA operands. All 16 table reads
+// are issued before any is used, so one LDS round trip covers the chunk.
+__device__ __forceinline__ void nf4_16bytes_to_bf16(const float2* tab, u32x4_t w, unsigned lane_off,
+                                                    float s, u32x4_t (&out)[4]) {
+  float2 p[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned addr = __builtin_amdgcn_perm(w[j], lane_off, 0x0C0C0000u | ((4u + i) << 8));
+      p[4 * j + i] = *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(tab) + addr);
+    }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[j][i] = bf16x2_bits(p[4 * j + i].x * s, p[4 * j + i].y * s);
 }
 
 // 8 MXFP4 elements of one packed dword (low nibble first) -> 4 bf16 pairs.
@@ -149,7 +182,7 @@ struct FwdArgs {
   const void* S;            // absmax f32 [E, N, K/64] or e8m0 u8 [E, N, K/32]
   int64_t sse, ssn;         // elements
   const int32_t* eids;      // [G]
-  const int32_t* row_off;   // [G + 1]
+  const int32_t* row_off;   // [G + 1], or null: group g is the single row g
   const int32_t* t_row0;    // [n_mtiles] (gemm path)
   const int32_t* t_rows;
   const int32_t* t_group;
@@ -161,7 +194,36 @@ struct FwdArgs {
 };
 
 constexpr int kDecodeWaves = 4;
-constexpr int kRing = 4;  // chunks in flight per wave (16 B weight + 64 B act per lane each)
+constexpr int kOOB = (int)0x80000000;  // buffer offset past every resource: loads 0
+
+// Buffer resources: raw loads through them are bounds-checked by the
+// hardware, so a masked lane gets zeros without a branch (and the compiler
+// keeps exact vmcnt counts for the prefetched loads).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes < 0x7FFFFFFF ? (int)bytes : 0x7FFFFFFF;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ unsigned buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+
+__device__ __forceinline__ unsigned buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0);
+}
+
+// off | 0x80000000 when !ok, through an opaque VALU op so the compiler cannot
+// turn the masked load back into a branch around two loads.
+__device__ __forceinline__ int oob_unless(bool ok, int off) {
+  const int mask = ok ? 0 : kOOB;
+  int r;
+  asm volatile("v_or_b32 %0, %1, %2" : "=v"(r) : "v"(off), "v"(mask));
+  return r;
+}
 
 template <int FMT>
 __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t n, int64_t k) {
@@ -174,87 +236,123 @@ __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t
   }
 }
 
-template <int FMT>
+// Decode path. A unit is (group g, 16-row weight tile); the workgroup's four
+// waves split the unit's 128-element K chunks round-robin (wave w takes
+// chunks w, w+4, ...; kChunksPerWave per round), each issuing all its weight, scale and activation
+// loads before the first wait, then reduce their 16 x 16 partial tiles
+// through LDS in wave order (deterministic). Lane (nl, q) carries weight row
+// nl of the tile and activation row nl of the group, k-segment q (32
+// elements = 16 packed bytes) of each chunk.
+template <int FMT, int kChunksPerWave, int kTiles>
 __global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
   __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
-  if constexpr (FMT == kNF4) {
-    init_pair_table(s_tab);
-    __syncthreads();
-  }
+  __shared__ f32x4_t s_red[kDecodeWaves - 1][kTiles][64];
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int nl = lane & 15;   // weight row within the tile / activation row
-  const int q = lane >> 4;    // 32-element segment of a 128-element chunk
+  const int nl = lane & 15;
+  const int q = lane >> 4;
   const unsigned lane_off = (unsigned)(lane & 31) * 8u;
-  const int64_t n_tiles = (p.N + 15) >> 4;
-  const int64_t units = (int64_t)p.G * n_tiles;
-  const int64_t nchunks = (p.K + 127) >> 7;
+  const int64_t n_units = (p.N + 16 * kTiles - 1) / (16 * kTiles);
+  const int64_t u = blockIdx.x;  // one unit per workgroup
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
 
-  for (int64_t u = (int64_t)blockIdx.x * kDecodeWaves + wave; u < units;
-       u += (int64_t)gridDim.x * kDecodeWaves) {
-    const int g = (int)(u / n_tiles);
-    const int64_t nt = u - (int64_t)g * n_tiles;
-    const int r0 = p.row_off[g];
-    const int M = p.row_off[g + 1] - r0;
-    if (M <= 0) continue;
-    const int64_t e = p.eids[g];
-    const int64_t n = nt * 16 + nl;
-    const int64_t nc = n < p.N ? n : p.N - 1;
-    const uint8_t* brow = p.B + e * p.sbe + nc * p.sbn;
-    const bool mval = nl < M;
-    const uint16_t* arow = p.a + (int64_t)(r0 + (mval ? nl : 0)) * p.lda;
+  const int g = (int)(u / n_units);
+  const int64_t nu = u - (int64_t)g * n_units;
+  const int r0 = p.row_off ? p.row_off[g] : g;
+  const int M = p.row_off ? p.row_off[g + 1] - r0 : 1;
+  if (M <= 0) return;  // uniform across the workgroup (empty group)
+  const int64_t e = p.eids[g];
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+      static_cast<const char*>(p.S) + e * p.sse * kScaleBytes, p.N * p.ssn * kScaleBytes);
+  // rows >= M fall outside this resource and load as zeros
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
+  // 32-bit per-lane byte offsets inside the resources (each < 2^31)
+  int b_row[kTiles], s_row[kTiles];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) {
+    const int64_t n = (nu * kTiles + t) * 16 + nl;
+    b_row[t] = n < p.N ? (int)(n * p.sbn) : kOOB;
+    s_row[t] = n < p.N ? (int)(n * p.ssn * kScaleBytes) : kOOB;
+  }
+  const int a_row = (int)((int64_t)nl * p.lda * 2);
+  const int K32 = (int)p.K;
+  const int nchunks = (K32 + 127) >> 7;
 
-    u32x4_t wb[kRing];
-    u32x4_t ab[kRing][4];
-    float sb[kRing];
-    auto issue = [&](int slot, int64_t c) {
-      const int64_t kseg = c * 128 + q * 32;
-      const bool kval = c < nchunks && kseg < p.K;
-      if (kval) {
-        wb[slot] = *reinterpret_cast<const u32x4_t*>(brow + (kseg >> 1));
-        sb[slot] = load_scale<FMT>(p, e, nc, kseg);
-      } else {
-        wb[slot] = u32x4_t{0u, 0u, 0u, 0u};
-        sb[slot] = 0.0f;
+  f32x4_t acc[kTiles][2];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // One round: this wave's chunks c0, c0 + 4, ... (kChunksPerWave of them).
+  // All loads first, then (first round only) the table build, then compute.
+  auto round = [&](int c0, bool build_table) {
+    u32x4_t wb[kChunksPerWave][kTiles];
+    unsigned sb[kChunksPerWave][kTiles];
+    u32x4_t ab[kChunksPerWave][4];
+#pragma unroll
+    for (int i = 0; i < kChunksPerWave; ++i) {
+      const unsigned kseg = (unsigned)((c0 + i * kDecodeWaves) * 128 + q * 32);
+      const bool kval = kseg < (unsigned)K32;   // also false past the last chunk
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        wb[i][t] = buf_load16(rb, oob_unless(kval, b_row[t] + (int)(kseg >> 1)));
+        const int soff =
+            oob_unless(kval, s_row[t] + (int)(kseg >> (FMT == kNF4 ? 6 : 5)) * kScaleBytes);
+        sb[i][t] = FMT == kNF4 ? buf_load4(rs, soff) : buf_load1(rs, soff);
       }
+      const int aoff = oob_unless(kval, a_row + (int)kseg * 2);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        ab[slot][j] = (kval && mval) ? load_a8(arow + kseg + 8 * j) : u32x4_t{0u, 0u, 0u, 0u};
-    };
-#pragma unroll
-    for (int s = 0; s < kRing; ++s) issue(s, s);
-
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t c0 = 0; c0 < nchunks; c0 += kRing) {
-#pragma unroll
-      for (int s = 0; s < kRing; ++s) {
-        const u32x4_t w = wb[s];
-        const float sc = sb[s];
-        u32x4_t a0 = ab[s][0], a1 = ab[s][1], a2 = ab[s][2], a3 = ab[s][3];
-        issue(s, c0 + s + kRing);
-        u32x4_t b0, b1, b2, b3;
-        if constexpr (FMT == kNF4) {
-          b0 = nf4_dword_to_bf16(s_tab, w[0], lane_off, sc);
-          b1 = nf4_dword_to_bf16(s_tab, w[1], lane_off, sc);
-          b2 = nf4_dword_to_bf16(s_tab, w[2], lane_off, sc);
-          b3 = nf4_dword_to_bf16(s_tab, w[3], lane_off, sc);
-        } else {
-          b0 = mx_dword_to_bf16(w[0], sc);
-          b1 = mx_dword_to_bf16(w[1], sc);
-          b2 = mx_dword_to_bf16(w[2], sc);
-          b3 = mx_dword_to_bf16(w[3], sc);
-        }
-        acc = mfma(a0, b0, acc);
-        acc = mfma(a1, b1, acc);
-        acc = mfma(a2, b2, acc);
-        acc = mfma(a3, b3, acc);
+      for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the load block ahead of all use
+    if constexpr (FMT == kNF4) {
+      if (build_table) {  // built while the loads above are in flight
+        init_pair_table(s_tab, lut);
+        __syncthreads();
       }
     }
-    if (n < p.N) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 4 * q + i;
-        if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(acc[i]);
+    for (int i = 0; i < kChunksPerWave; ++i) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        u32x4_t b[4];
+        if constexpr (FMT == kNF4) {
+          nf4_16bytes_to_bf16(s_tab, wb[i][t], lane_off, __uint_as_float(sb[i][t]), b);
+        } else {
+          const float sc = e8m0_to_f32(sb[i][t]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) b[j] = mx_dword_to_bf16(wb[i][t][j], sc);
+        }
+        acc[t][0] = mfma(ab[i][0], b[0], acc[t][0]);
+        acc[t][1] = mfma(ab[i][1], b[1], acc[t][1]);
+        acc[t][0] = mfma(ab[i][2], b[2], acc[t][0]);
+        acc[t][1] = mfma(ab[i][3], b[3], acc[t][1]);
+      }
+    }
+  };
+  round(wave, true);  // every wave runs it: chunks past the end load zeros
+  for (int c0 = wave + kDecodeWaves * kChunksPerWave; c0 < nchunks;
+       c0 += kDecodeWaves * kChunksPerWave)
+    round(c0, false);
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) s_red[wave - 1][t][lane] = acc[t][0] + acc[t][1];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+      const int64_t n = (nu * kTiles + t) * 16 + nl;
+      const f32x4_t v =
+          (((acc[t][0] + acc[t][1]) + s_red[0][t][lane]) + s_red[1][t][lane]) + s_red[2][t][lane];
+      if (n < p.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * q + i;
+          if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+        }
       }
     }
   }
@@ -346,7 +444,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
   __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kLdsRow];
-  if constexpr (FMT == kNF4) init_pair_table(s_tab);
+  if constexpr (FMT == kNF4) init_pair_table(s_tab, nf4_lut_lane());
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -516,7 +614,7 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm_dgrad(const DgradArgs p) {
   __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kDgBK * kLdsRow];
-  if constexpr (FMT == kNF4) init_pair_table(s_tab);
+  if constexpr (FMT == kNF4) init_pair_table(s_tab, nf4_lut_lane());
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -621,10 +719,18 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
   if (p.n_mtiles == 0) {
-    // decode path: units = G x ceil(N / 16), 4 per workgroup, 2 workgroups/CU
-    const int64_t units = (int64_t)p.G * ((p.N + 15) / 16);
-    const int64_t grid = clamp_grid((units + kDecodeWaves - 1) / kDecodeWaves, (int64_t)cus * 2);
-    hipLaunchKernelGGL(k_decode_fwd<FMT>, dim3((unsigned)grid), dim3(256), 0, stream, p);
+    // decode path: one workgroup per unit (group, 32-row tile pair)
+    constexpr int kT = 2;
+    const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
+    if (grid > 0x7FFFFFFF) return -1;
+    // chunks of 128 k per wave: enough to cover K in one round where possible
+    const int64_t per_wave = ((p.K + 127) / 128 + kDecodeWaves - 1) / kDecodeWaves;
+    if (per_wave <= 2)
+      hipLaunchKernelGGL((k_decode_fwd<FMT, 2, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    else if (per_wave <= 4)
+      hipLaunchKernelGGL((k_decode_fwd<FMT, 4, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((k_decode_fwd<FMT, 6, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
   } else {
     const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kBN - 1) / kBN);
     const int64_t grid = clamp_grid(tiles, cus);
@@ -681,7 +787,6 @@ int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const
   if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
       !aligned16(a))
     return -1;
-  if (n_mtiles == 0 && !row_off) return -1;
   if (n_mtiles > 0 && (!t_row0 || !t_rows || !t_group)) return -1;
   FwdArgs p;
   p.a = static_cast<const uint16_t*>(a);

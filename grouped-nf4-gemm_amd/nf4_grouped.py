@@ -401,13 +401,20 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     eids_dev = _eids_device(expert_ids, dev)
     host_eids = [] if eids_dev is not None else expert_ids
     if max_m <= DECODE_MAX_ROWS and block_m is None:
-        row_off = [0]
-        for m in sizes_i:
-            row_off.append(row_off[-1] + m)
-        e_h, r_h = to_device_i32((host_eids, row_off), dev)
+        if min(sizes_i) == 1 and max_m == 1:
+            # one row per group: group g is row g, no offset table to upload
+            (e_h,) = to_device_i32((host_eids,), dev)
+            r_ptr = None
+            keep = (e_h,)
+        else:
+            row_off = [0]
+            for m in sizes_i:
+                row_off.append(row_off[-1] + m)
+            e_h, r_h = to_device_i32((host_eids, row_off), dev)
+            r_ptr = r_h.data_ptr()
+            keep = (e_h, r_h)
         eids = eids_dev if eids_dev is not None else e_h
-        args = (eids.data_ptr(), r_h.data_ptr(), G, None, None, None, 0, 0)
-        keep = (e_h, r_h, eids)
+        args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, 0)
     else:
         bm = _kernel_block_m(block_m if block_m is not None else _prefill_block_m(max_m))
         t0, tr, tg = _tiles_host(sizes_i, bm)

@@ -1,0 +1,323 @@
+"""Pin the CPU oracle (oracle/) before trusting it as the GPU checker.
+
+What pins what (reference files cited inline):
+  * codebooks   -- the reference's literal values; transformers' FP4_VALUES.
+  * decode      -- closed-form nibble order over all 256 bytes; MXFP4 byte
+                   0x21 known answer; transformers' own MXFP4 dequant; e8m0
+                   0x00 / 0xFF edges.
+  * locked tree -- C oracle == numpy spec == the reference's compiled CPU
+                   kernels (oracle/_ref) == the golden vectors those kernels
+                   wrote (tests/golden), bit for bit; thread count invariance;
+                   an independent fp64 check (catches a shared misreading).
+  * packers     -- argmin / first-index-on-ties by brute force; round trip.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import native, spec
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+E, N, K = 4, 24, 128
+SIZES = [1, 2, 1]
+EIDS = [2, 0, 3]
+
+# the reference's literal codebooks, kernel/nf4_grouped.py:53-70 and
+# kernel/mxfp4_pack_ref.py:21-22
+NF4_REF = [-1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+           -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+           0.07958029955625534, 0.16093020141124725, 0.24611230194568634,
+           0.33791524171829224, 0.44070982933044434, 0.5626170039176941,
+           0.7229568362236023, 1.0]
+FP4_REF = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
+           -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+
+
+def nanfix(x):
+    return np.nan_to_num(np.asarray(x), nan=1e30, posinf=2e30, neginf=-2e30)
+
+
+def nf4_stack(seed, rows, k=K):
+    g = np.random.default_rng(seed)
+    packed = g.integers(0, 256, size=(E, N, k // 2), dtype=np.uint8)
+    absmax = g.random(size=(E, N, k // 64), dtype=np.float32) + 0.5
+    a = g.standard_normal((rows, k), dtype=np.float32)
+    return a, packed, absmax
+
+
+def mx_stack(seed, rows, weird=False, k=K):
+    g = np.random.default_rng(seed)
+    packed = g.integers(0, 256, size=(E, N, k // 2), dtype=np.uint8)
+    scales = g.integers(100, 140, size=(E, N, k // 32), dtype=np.uint8)
+    if weird:
+        scales[0, 0, 0] = 0xFF
+        scales[0, 0, 1] = 0
+        scales[1, 3, scales.shape[2] - 1] = 0xFF
+    a = g.standard_normal((rows, k), dtype=np.float32)
+    return a, packed, scales
+
+
+# ---------------------------------------------------------------- codebooks --
+
+def test_codebooks_match_the_reference_literals_everywhere():
+    import mxfp4_grouped
+    import mxfp4_pack_ref
+    import nf4_grouped
+    nf4_c, fp4_c = native.oracle_luts()
+    want_nf4 = np.asarray(NF4_REF, dtype=np.float32)
+    want_fp4 = np.asarray(FP4_REF, dtype=np.float32)
+    for got in (nf4_c, spec.NF4_LUT32, np.asarray(nf4_grouped.NF4_LUT, np.float32)):
+        assert np.array_equal(got.view(np.uint32), want_nf4.view(np.uint32))
+    for got in (fp4_c, spec.FP4_LUT32, np.asarray(mxfp4_grouped.FP4_VALUES, np.float32),
+                np.asarray(mxfp4_pack_ref.FP4_VALUES, np.float32)):
+        assert np.array_equal(got.view(np.uint32), want_fp4.view(np.uint32))  # -0.0 too
+    assert nf4_grouped.BLOCKSIZE == spec.BLOCKSIZE == 64
+    assert mxfp4_grouped.MX_BLOCK == spec.MX_BLOCK == 32 and mxfp4_grouped.E8M0_BIAS == 127
+    assert spec.NF4_LUT32[7] == 0.0 and np.all(np.diff(spec.NF4_LUT32) > 0)
+
+
+def test_fp4_codebook_matches_transformers():
+    M = pytest.importorskip("transformers.integrations.mxfp4")
+    assert list(M.FP4_VALUES) == FP4_REF
+
+
+# ------------------------------------------------------------------- decode --
+
+def test_nibble_order_closed_form_over_all_bytes():
+    b = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    nf = spec.codes_nf4(b)[0]
+    mx = spec.codes_mxfp4(b)[0]
+    for v in range(256):
+        assert (nf[2 * v], nf[2 * v + 1]) == (v >> 4, v & 15)     # NF4: 2j = HIGH
+        assert (mx[2 * v], mx[2 * v + 1]) == (v & 15, v >> 4)     # MXFP4: 2j = LOW
+
+
+def test_mxfp4_byte_0x21_known_answer():
+    # reference kernel/test_mxfp4_oracle.py:51-71: low nibble 1 -> 0.5, high 2 -> 1.0
+    blocks = np.zeros((1, 16), dtype=np.uint8)
+    blocks[0, 0] = 0x21
+    w = spec.dequant_mxfp4(blocks, np.full((1, 1), 127, np.uint8))
+    assert (w[0, 0], w[0, 1]) == (0.5, 1.0) and not np.any(w[0, 2:])
+
+
+def test_e8m0_edges():
+    blocks = np.full((1, 16), 0x21, dtype=np.uint8)
+    w0 = spec.dequant_mxfp4(blocks, np.zeros((1, 1), np.uint8))
+    assert w0[0, 0] == np.float32(2.0 ** -128) and w0[0, 1] == np.float32(2.0 ** -127)
+    blocks[0, 1] = 0x00
+    with np.errstate(over="ignore"):
+        wf = spec.dequant_mxfp4(blocks, np.full((1, 1), 255, np.uint8))
+    # 0.5 * 2^128 = 2^127 is finite, 1.0 * 2^128 overflows; ldexp keeps 0 at 0
+    assert wf[0, 0] == np.float32(2.0 ** 127) and np.isinf(wf[0, 1])
+    assert wf[0, 2] == 0.0 and wf[0, 3] == 0.0
+
+
+def test_nf4_decode_is_one_rounding_of_lut_times_absmax():
+    g = np.random.default_rng(3)
+    packed = g.integers(0, 256, size=(5, 96), dtype=np.uint8)
+    absmax = (g.random(size=(5, 3)) * 10).astype(np.float32)
+    w = spec.dequant_nf4(packed, absmax)
+    for r in range(5):
+        for k in range(192):
+            byte = packed[r, k // 2]
+            c = byte >> 4 if k % 2 == 0 else byte & 15
+            assert w[r, k] == np.float32(NF4_REF[c]) * absmax[r, k // 64]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 7])
+def test_mxfp4_decode_matches_transformers(seed):
+    torch = pytest.importorskip("torch")
+    M = pytest.importorskip("transformers.integrations.mxfp4")
+    fn = getattr(M, "_convert_moe_packed_tensors", None)
+    if fn is None:
+        pytest.skip("transformers lacks _convert_moe_packed_tensors")
+    g = np.random.default_rng(seed)
+    blocks = g.integers(0, 256, size=(3, 4, 16), dtype=np.uint8)
+    scales = g.integers(115, 140, size=(3, 4), dtype=np.uint8)
+    ref = fn(torch.from_numpy(blocks).unsqueeze(0), torch.from_numpy(scales).unsqueeze(0),
+             dtype=torch.float32, rows_per_chunk=1 << 30)
+    ref = ref.transpose(1, 2).reshape(3, 4 * 32).numpy()
+    ours = spec.dequant_mxfp4(blocks.reshape(3, 64), scales)
+    assert np.array_equal(ours, ref)
+
+
+def test_package_reference_decoders_match_the_spec():
+    torch = pytest.importorskip("torch")
+    from mxfp4_pack_ref import dequant_mxfp4
+    from nf4_grouped import dequant_ref
+    g = np.random.default_rng(11)
+    packed = g.integers(0, 256, size=(7, 64), dtype=np.uint8)
+    absmax = (g.random(size=(7, 2)) + 0.1).astype(np.float32)
+    got = dequant_ref(torch.from_numpy(packed), torch.from_numpy(absmax), 7, 128).numpy()
+    assert np.array_equal(got, spec.dequant_nf4(packed, absmax))
+    scales = g.integers(90, 160, size=(7, 4), dtype=np.uint8)
+    got = dequant_mxfp4(torch.from_numpy(packed.reshape(7, 4, 16)), torch.from_numpy(scales)).numpy()
+    assert np.array_equal(got, spec.dequant_mxfp4(packed, scales))
+
+
+# -------------------------------------------------------------- locked tree --
+
+def test_c_oracle_equals_numpy_spec_nf4():
+    a, p, s = nf4_stack(0, sum(SIZES))
+    assert np.array_equal(native.gemv_grouped(a, p, s, SIZES, EIDS, fmt="nf4"),
+                          spec.ref_gemv_grouped(a, p, s, SIZES, EIDS, fmt="nf4"))
+
+
+@pytest.mark.parametrize("weird", [False, True])
+def test_c_oracle_equals_numpy_spec_mxfp4(weird):
+    a, p, s = mx_stack(1, sum(SIZES), weird)
+    with np.errstate(over="ignore"):
+        want = spec.ref_gemv_grouped(a, p, s, SIZES, EIDS, fmt="mxfp4")
+    assert np.array_equal(nanfix(native.gemv_grouped(a, p, s, SIZES, EIDS, fmt="mxfp4")), nanfix(want))
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("sizes", [[9], [16], [8, 17, 1], [33, 2], [3, 0, 5]])
+def test_large_and_empty_groups_equal_the_spec(fmt, sizes):
+    eids = [i % E for i in range(len(sizes))]
+    a, p, s = (nf4_stack(0, sum(sizes)) if fmt == "nf4" else mx_stack(1, sum(sizes)))
+    assert np.array_equal(native.gemv_grouped(a, p, s, sizes, eids, fmt=fmt),
+                          spec.ref_gemv_grouped(a, p, s, sizes, eids, fmt=fmt))
+
+
+@pytest.mark.parametrize("k", [64, 128, 192, 320])
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_dgrad_c_oracle_equals_spec(fmt, k):
+    _, p, s = nf4_stack(17, 1, k=k) if fmt == "nf4" else mx_stack(17, 1, weird=True, k=k)
+    g = np.random.default_rng(k).standard_normal((sum(SIZES), N), dtype=np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = spec.ordered_dgrad_ref(g, p, s, SIZES, EIDS, fmt=fmt)
+    got = native.dgrad_grouped(g, p, s, SIZES, EIDS, fmt=fmt)
+    assert np.array_equal(nanfix(got), nanfix(want))
+
+
+def test_thread_count_does_not_change_bits():
+    a, p, s = nf4_stack(7, 40)
+    sizes, eids = [13, 20, 7], [1, 3, 0]
+    one = native.gemv_grouped(a, p, s, sizes, eids, fmt="nf4", threads=1)
+    four = native.gemv_grouped(a, p, s, sizes, eids, fmt="nf4", threads=4)
+    assert np.array_equal(one, four)
+    g = np.random.default_rng(8).standard_normal((40, N), dtype=np.float32)
+    assert np.array_equal(native.dgrad_grouped(g, p, s, sizes, eids, fmt="nf4", threads=1),
+                          native.dgrad_grouped(g, p, s, sizes, eids, fmt="nf4", threads=3))
+
+
+def _golden_cases():
+    return sorted(GOLDEN.glob("*.npz"))
+
+
+@pytest.mark.parametrize("path", _golden_cases(), ids=lambda p: p.stem)
+def test_c_oracle_reproduces_the_reference_golden_vectors(path):
+    """Vectors written by the reference's compiled CPU kernels."""
+    z = np.load(path)                       # allow_pickle stays False
+    op, fmt = str(z["op"]), str(z["fmt"])
+    sizes, eids = z["sizes"].tolist(), z["eids"].tolist()
+    fn = native.gemv_grouped if op == "gemv" else native.dgrad_grouped
+    got = fn(z["x"], z["packed"], z["scales"], sizes, eids, fmt=fmt)
+    assert np.array_equal(nanfix(got), nanfix(z["out"]))
+
+
+def test_golden_set_is_complete():
+    names = {p.stem for p in _golden_cases()}
+    assert {"gemv_nf4_fixture", "gemv_mxfp4_weird_scales", "dgrad_nf4_fixture",
+            "dgrad_mxfp4_weird_scales", "gemv_nf4_config1_slice"} <= names
+
+
+needs_ref = pytest.mark.skipif(native.ref_lib() is None, reason="oracle/_ref not built here")
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [0, 5, 9])
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_c_oracle_equals_the_compiled_reference_live(fmt, seed):
+    rng = np.random.default_rng(seed)
+    sizes = [int(x) for x in rng.integers(1, 12, size=5)]
+    eids = [int(x) for x in rng.integers(0, E, size=5)]
+    a, p, s = nf4_stack(seed, sum(sizes), k=256) if fmt == "nf4" else mx_stack(seed, sum(sizes), True, k=256)
+    got = native.gemv_grouped(a, p, s, sizes, eids, fmt=fmt)
+    ref = native.ref_gemv_grouped(a, p, s, sizes, eids, fmt=fmt)
+    assert np.array_equal(nanfix(got), nanfix(ref))
+    g = rng.standard_normal((sum(sizes), N), dtype=np.float32)
+    assert np.array_equal(nanfix(native.dgrad_grouped(g, p, s, sizes, eids, fmt=fmt)),
+                          nanfix(native.ref_dgrad_grouped(g, p, s, sizes, eids, fmt=fmt)))
+
+
+# ---------------------------------------------- independent fp64 agreement --
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_forward_agrees_with_fp64(fmt):
+    a, p, s = nf4_stack(3, 20, k=512) if fmt == "nf4" else mx_stack(3, 20, k=512)
+    sizes, eids = [6, 9, 5], [0, 2, 3]
+    got = native.gemv_grouped(a, p, s, sizes, eids, fmt=fmt)
+    want = spec.fp64_forward(a, p, s, sizes, eids, fmt=fmt)
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_dgrad_is_the_forward_transpose(fmt):
+    """<dX, x> == <dY, W x> per group in fp64: a transposed or mis-indexed
+    dgrad fails this, whatever the summation order."""
+    _, p, s = nf4_stack(11, 1, k=256) if fmt == "nf4" else mx_stack(11, 1, k=256)
+    sizes, eids = [4, 7], [1, 3]
+    rng = np.random.default_rng(12)
+    dy = rng.standard_normal((11, N), dtype=np.float32)
+    x = rng.standard_normal((11, 256), dtype=np.float32)
+    dx = native.dgrad_grouped(dy, p, s, sizes, eids, fmt=fmt).astype(np.float64)
+    wx = spec.fp64_forward(x, p, s, sizes, eids, fmt=fmt)
+    lhs = np.sum(dx * x.astype(np.float64))
+    rhs = np.sum(dy.astype(np.float64) * wx)
+    assert abs(lhs - rhs) <= 1e-4 * (abs(rhs) + 1)
+
+
+def test_one_hot_rows_reduce_to_the_decode():
+    """A one-hot activation turns the locked tree into a single product: the
+    output is the decoded weight exactly."""
+    _, p, s = nf4_stack(21, 1, k=256)
+    a = np.zeros((3, 256), dtype=np.float32)
+    cols = [0, 131, 255]
+    for r, c in enumerate(cols):
+        a[r, c] = 1.0
+    out = native.gemv_grouped(a, p, s, [3], [2], fmt="nf4")
+    w = spec.dequant_nf4(p[2], s[2])
+    for r, c in enumerate(cols):
+        assert np.array_equal(out[r], w[:, c])
+
+
+# ------------------------------------------------------------------ packers --
+
+def test_nf4_packer_is_nearest_code_first_index_on_ties():
+    torch = pytest.importorskip("torch")
+    from nf4_pack_ref import quantize_pack_nf4
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(6, 128, generator=g)
+    w[0, 5] = 0.0                 # exact code 7
+    w[1, :64] = 0.0               # all-zero block -> absmax clamp
+    packed, absmax = quantize_pack_nf4(w)
+    assert absmax[1, 0].item() == pytest.approx(1e-12)
+    lut = np.asarray(NF4_REF, np.float32)
+    codes = spec.codes_nf4(packed.numpy())
+    am = absmax.numpy()
+    for r in range(6):
+        for k in range(128):
+            x = np.float32(w[r, k].item()) / am[r, k // 64]
+            d = np.abs(np.float32(x) - lut)
+            assert codes[r, k] == int(np.argmin(d))     # numpy argmin: first index on ties
+    assert codes[0, 5] == 7
+
+
+def test_packers_round_trip():
+    torch = pytest.importorskip("torch")
+    from mxfp4_pack_ref import dequant_mxfp4, quantize_pack_mxfp4
+    from nf4_grouped import dequant_ref
+    from nf4_pack_ref import quantize_pack_nf4
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(64, 256, generator=g)
+    p, a = quantize_pack_nf4(w)
+    rel = ((dequant_ref(p, a, 64, 256) - w).norm() / w.norm()).item()
+    assert 0.05 < rel < 0.12          # reference README: ~0.09
+    b, s = quantize_pack_mxfp4(w)
+    rel = ((dequant_mxfp4(b, s) - w).norm() / w.norm()).item()
+    assert 0.05 < rel < 0.16          # reference README: ~0.12
+    assert (s.int() - 127).abs().max().item() <= 127

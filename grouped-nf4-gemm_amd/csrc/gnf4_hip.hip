@@ -87,16 +87,18 @@ __device__ __forceinline__ int nf4_lut_lane() {
 }
 
 __device__ __forceinline__ void init_pair_table(float2* tab, int lut) {
-  // Thread t (of the 256 every kernel here launches) fills the 32 columns of
-  // byte t, rotating the column order by byte so one store instruction
+  // Thread t fills the columns of byte t % 256 (all 32 of them with 256
+  // threads, half of them with 512), rotating the column order by byte so one store instruction
   // touches distinct banks. Entries come from the codebook register of lanes
   // 0..15 through ds_bpermute.
-  const unsigned b = threadIdx.x;
+  const unsigned b = threadIdx.x & 255;
   const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b >> 4) << 2), lut));
   const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b & 15) << 2), lut));
   const float2 e = make_float2(hi, lo);
-#pragma unroll
-  for (int j = 0; j < 32; ++j) tab[b * 32 + ((j + b) & 31)] = e;
+  // with 512 threads the second 256 fill the other half of the columns
+  const int j0 = threadIdx.x < 256 ? 0 : 16;
+  const int nj = blockDim.x > 256 ? 16 : 32;
+  for (int j = 0; j < nj; ++j) tab[b * 32 + ((j0 + j + b) & 31)] = e;
 }
 
 __device__ __forceinline__ unsigned bf16x2_bits(float lo, float hi) {
@@ -188,12 +190,12 @@ struct FwdArgs {
   const int32_t* t_group;
   int n_mtiles;
   int G;
+  int max_m;                // largest group (decode path)
   int64_t N, K;
   uint16_t* out;            // [T, ldo] bf16
   int64_t ldo;
 };
 
-constexpr int kDecodeWaves = 4;
 constexpr int kOOB = (int)0x80000000;  // buffer offset past every resource: loads 0
 
 // Buffer resources: raw loads through them are bounds-checked by the
@@ -236,19 +238,32 @@ __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t
   }
 }
 
-// Decode path. A unit is (group g, 16-row weight tile); the workgroup's four
-// waves split the unit's 128-element K chunks round-robin (wave w takes
-// chunks w, w+4, ...; kChunksPerWave per round), each issuing all its weight, scale and activation
-// loads before the first wait, then reduce their 16 x 16 partial tiles
-// through LDS in wave order (deterministic). Lane (nl, q) carries weight row
-// nl of the tile and activation row nl of the group, k-segment q (32
-// elements = 16 packed bytes) of each chunk.
-template <int FMT, int kChunksPerWave, int kTiles>
-__global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
-  __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
-  __shared__ f32x4_t s_red[kDecodeWaves - 1][kTiles][64];
+// Decode path. A unit is (group g, kTiles x 16 weight rows). The
+// workgroup's kDecodeWaves waves split the unit's 128-element K chunks into
+// contiguous runs (wave w takes chunks w * kChunksPerWave, ...). Every buffer
+// load costs the CU's vector-memory front end about the same whatever its
+// lane mask, so the kernel keeps their number low:
+//   * with kAPieces > 0 (groups of at most two rows) the group's activation
+//     rows are staged once per workgroup into LDS (a few 16-byte loads per
+//     thread) in a [k / 8][row] layout and each MFMA A operand is a 16-byte
+//     LDS read (rows >= M read a zero block); with kAPieces == 0 (larger
+//     groups, where most lanes carry a row) the operands are loaded straight
+//     into registers with the weights;
+//   * each weight load moves 16 bytes per lane (32 elements of one row);
+//   * an NF4 lane's absmax values for a whole run are one 16-byte load;
+// and issues all of them before the first wait. The waves then reduce their
+// 16 x 16 partial tiles through LDS in wave order (deterministic).
+//
+// Dynamic LDS: [NF4 pair table 64 KiB][activations M * K * 2][zero block];
+// the reduction buffer reuses the start once the table is no longer read.
+template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces>
+// two workgroups per CU: kDecodeWaves / 2 waves per SIMD
+__global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_fwd(const FwdArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float2* s_tab = reinterpret_cast<float2*>(smem);
   const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
   __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
+  constexpr int kThreadsD = 64 * kDecodeWaves;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nl = lane & 15;
@@ -264,12 +279,28 @@ __global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
   const int M = p.row_off ? p.row_off[g + 1] - r0 : 1;
   if (M <= 0) return;  // uniform across the workgroup (empty group)
   const int64_t e = p.eids[g];
+  const int K32 = (int)p.K;
+  const int kslices = K32 >> 3;                       // 16-byte activation pieces per row
+  const int a_base = FMT == kNF4 ? 8 * kPairEntries : 0;
+  const int zero_off = a_base + ((M * kslices * 16 + 15) & ~15);
+
+  // ---- activation staging loads (first in the queue: they are waited on first)
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
+  const int pieces = M * kslices;
+  u32x4_t av[kAPieces > 0 ? kAPieces : 1];
+#pragma unroll
+  for (int i = 0; i < kAPieces; ++i) {
+    const int pc = (int)threadIdx.x + i * kThreadsD;
+    if (wave * 64 + i * kThreadsD < pieces) {         // uniform: whole waves skip
+      const int m = pc / kslices, sl = pc - m * kslices;
+      av[i] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+    }
+  }
+
+  // ---- weight and scale loads
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(
       static_cast<const char*>(p.S) + e * p.sse * kScaleBytes, p.N * p.ssn * kScaleBytes);
-  // rows >= M fall outside this resource and load as zeros
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
-  // 32-bit per-lane byte offsets inside the resources (each < 2^31)
   int b_row[kTiles], s_row[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
@@ -277,44 +308,88 @@ __global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
     b_row[t] = n < p.N ? (int)(n * p.sbn) : kOOB;
     s_row[t] = n < p.N ? (int)(n * p.ssn * kScaleBytes) : kOOB;
   }
-  const int a_row = (int)((int64_t)nl * p.lda * 2);
-  const int K32 = (int)p.K;
   const int nchunks = (K32 + 127) >> 7;
 
   f32x4_t acc[kTiles][2];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // One round: this wave's chunks c0, c0 + 4, ... (kChunksPerWave of them).
-  // All loads first, then (first round only) the table build, then compute.
-  auto round = [&](int c0, bool build_table) {
+  // One round: this wave's chunks c0 .. c0 + kChunksPerWave - 1. All loads
+  // first; in the first round the LDS staging (table, activations) happens
+  // while they are in flight.
+  static_assert(FMT != kNF4 || kChunksPerWave <= 2, "one 16-byte absmax load per run");
+  auto round = [&](int c0, bool first) {
     u32x4_t wb[kChunksPerWave][kTiles];
     unsigned sb[kChunksPerWave][kTiles];
-    u32x4_t ab[kChunksPerWave][4];
+    u32x4_t sv[kTiles];
+    u32x4_t ab[kAPieces == 0 ? kChunksPerWave : 1][4];
+    if constexpr (FMT == kNF4) {
+      // absmax blocks 2 * c0 .. 2 * c0 + 3 of the lane's row: chunk c0 + i,
+      // segment q uses block 2 * (c0 + i) + q / 2
+      const bool sval = (unsigned)(c0 * 128) < (unsigned)K32;
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        const int soff = oob_unless(sval, s_row[t] + c0 * 8);
+        sv[t] = buf_load16(rs, soff);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kChunksPerWave; ++i) {
-      const unsigned kseg = (unsigned)((c0 + i * kDecodeWaves) * 128 + q * 32);
+      const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
       const bool kval = kseg < (unsigned)K32;   // also false past the last chunk
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
         wb[i][t] = buf_load16(rb, oob_unless(kval, b_row[t] + (int)(kseg >> 1)));
-        const int soff =
-            oob_unless(kval, s_row[t] + (int)(kseg >> (FMT == kNF4 ? 6 : 5)) * kScaleBytes);
-        sb[i][t] = FMT == kNF4 ? buf_load4(rs, soff) : buf_load1(rs, soff);
+        if constexpr (FMT != kNF4)
+          sb[i][t] = buf_load1(rs, oob_unless(kval, s_row[t] + (int)(kseg >> 5)));
       }
-      const int aoff = oob_unless(kval, a_row + (int)kseg * 2);
+      if constexpr (kAPieces == 0) {
+        // rows >= M fall outside the activation resource and load as zeros
+        const int aoff = oob_unless(kval, (int)((int64_t)nl * p.lda * 2) + (int)kseg * 2);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
+        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the load block ahead of all use
     if constexpr (FMT == kNF4) {
-      if (build_table) {  // built while the loads above are in flight
-        init_pair_table(s_tab, lut);
-        __syncthreads();
+#pragma unroll
+      for (int i = 0; i < kChunksPerWave; ++i)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+          const int idx = 2 * i + (q >> 1);   // 0..3
+          sb[i][t] = idx == 0 ? sv[t][0] : idx == 1 ? sv[t][1] : idx == 2 ? sv[t][2] : sv[t][3];
+        }
+    }
+    if (first) {
+      if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
+      if (kAPieces > 0 && threadIdx.x < 4)
+        *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < kAPieces; ++i) {
+        const int pc = (int)threadIdx.x + i * kThreadsD;
+        if (wave * 64 + i * kThreadsD < pieces && pc < pieces) {
+          const int m = pc / kslices, sl = pc - m * kslices;
+          *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m) * 16) = av[i];
+        }
       }
+      __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < kChunksPerWave; ++i) {
+      const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+      const bool kval = kseg < (unsigned)K32;
+      u32x4_t a[4];
+      if constexpr (kAPieces > 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int off =
+              (kval && nl < M) ? a_base + (((int)(kseg >> 3) + j) * M + nl) * 16 : zero_off;
+          a[j] = *reinterpret_cast<const u32x4_t*>(smem + off);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = ab[i][j];
+      }
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
         u32x4_t b[4];
@@ -325,34 +400,35 @@ __global__ void __launch_bounds__(256, 2) k_decode_fwd(const FwdArgs p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) b[j] = mx_dword_to_bf16(wb[i][t][j], sc);
         }
-        acc[t][0] = mfma(ab[i][0], b[0], acc[t][0]);
-        acc[t][1] = mfma(ab[i][1], b[1], acc[t][1]);
-        acc[t][0] = mfma(ab[i][2], b[2], acc[t][0]);
-        acc[t][1] = mfma(ab[i][3], b[3], acc[t][1]);
+        acc[t][0] = mfma(a[0], b[0], acc[t][0]);
+        acc[t][1] = mfma(a[1], b[1], acc[t][1]);
+        acc[t][0] = mfma(a[2], b[2], acc[t][0]);
+        acc[t][1] = mfma(a[3], b[3], acc[t][1]);
       }
     }
   };
-  round(wave, true);  // every wave runs it: chunks past the end load zeros
-  for (int c0 = wave + kDecodeWaves * kChunksPerWave; c0 < nchunks;
+  round(wave * kChunksPerWave, true);  // every wave runs it: chunks past the end load zeros
+  for (int c0 = (kDecodeWaves + wave) * kChunksPerWave; c0 < nchunks;
        c0 += kDecodeWaves * kChunksPerWave)
     round(c0, false);
-  if (wave > 0) {
+
+  __syncthreads();  // the table is no longer read: its space takes the partials
+  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem);   // [kDecodeWaves][kTiles][64]
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) s_red[wave - 1][t][lane] = acc[t][0] + acc[t][1];
-  }
+  for (int t = 0; t < kTiles; ++t) s_red[(wave * kTiles + t) * 64 + lane] = acc[t][0] + acc[t][1];
   __syncthreads();
-  if (wave == 0) {
+  // wave t < kTiles sums tile t over the waves in wave order (deterministic)
+  if (wave < kTiles) {
+    const int t = wave;
+    const int64_t n = (nu * kTiles + t) * 16 + nl;
+    f32x4_t v = s_red[t * 64 + lane];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-      const int64_t n = (nu * kTiles + t) * 16 + nl;
-      const f32x4_t v =
-          (((acc[t][0] + acc[t][1]) + s_red[0][t][lane]) + s_red[1][t][lane]) + s_red[2][t][lane];
-      if (n < p.N) {
+    for (int w = 1; w < kDecodeWaves; ++w) v = v + s_red[(w * kTiles + t) * 64 + lane];
+    if (n < p.N) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * q + i;
-          if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int m = 4 * q + i;
+        if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
       }
     }
   }
@@ -714,23 +790,71 @@ int device_cus() {
 
 int64_t clamp_grid(int64_t work, int64_t cap) { return work < cap ? (work > 0 ? work : 1) : cap; }
 
+// Launch one decode-kernel instance with `lds` bytes of dynamic LDS.
+template <int FMT, int CPW, int T, int W, int PA>
+int launch_decode_inst(const FwdArgs& p, int64_t grid, int lds, hipStream_t stream) {
+  static int configured_dev = -1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  if (configured_dev != dev) {   // allow more than the default 64 KiB of dynamic LDS
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode_fwd<FMT, CPW, T, W, PA>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return -2;
+    configured_dev = dev;
+  }
+  hipLaunchKernelGGL((k_decode_fwd<FMT, CPW, T, W, PA>), dim3((unsigned)grid), dim3(64 * W),
+                     lds, stream, p);
+  return 0;
+}
+
+template <int FMT, int CPW, int T>
+int launch_decode_pa(const FwdArgs& p, int64_t grid, int pa, int lds, hipStream_t stream) {
+  constexpr int W = 8;
+  switch (pa) {
+    case 1: return launch_decode_inst<FMT, CPW, T, W, 1>(p, grid, lds, stream);
+    case 2: return launch_decode_inst<FMT, CPW, T, W, 2>(p, grid, lds, stream);
+    case 4: return launch_decode_inst<FMT, CPW, T, W, 4>(p, grid, lds, stream);
+    default: return launch_decode_inst<FMT, CPW, T, W, 0>(p, grid, lds, stream);
+  }
+}
+
+// Decode launch: one workgroup of eight waves per unit (group, 32 rows).
+// Groups of at most two rows stage their activations in LDS; larger ones load
+// them into registers. NF4 runs at most two chunks per wave per round (its
+// absmax run load covers two), MXFP4 up to four.
+template <int FMT>
+int launch_decode(const FwdArgs& p, hipStream_t stream) {
+  constexpr int kW = 8, kT = 2;
+  const int64_t per_wave = ((p.K + 127) / 128 + kW - 1) / kW;
+  const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
+  if (grid > 0x7FFFFFFF) return -1;
+  const bool stage = p.max_m <= 2;
+  const int64_t a_bytes = stage ? (int64_t)p.max_m * p.K * 2 : 0;
+  const int64_t pieces = (a_bytes + 15) / 16;
+  const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
+  const int64_t red = (int64_t)kW * kT * 64 * 16;
+  const int64_t table = FMT == kNF4 ? 8 * kPairEntries : 0;
+  int64_t lds = table + ((a_bytes + 15) & ~15) + 64;
+  if (lds < red) lds = red;
+  if (lds > 160 * 1024) return -1;
+  if (per_wave <= 1) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, (int)lds, stream);
+  if constexpr (FMT == kNF4) {
+    return launch_decode_pa<FMT, 2, kT>(p, grid, pa, (int)lds, stream);
+  } else {
+    if (per_wave <= 2) return launch_decode_pa<FMT, 2, kT>(p, grid, pa, (int)lds, stream);
+    if (per_wave <= 3 || !stage)   // register operands: 3 chunks per round fit 128 VGPRs
+      return launch_decode_pa<FMT, 3, kT>(p, grid, pa, (int)lds, stream);
+    return launch_decode_pa<FMT, 4, kT>(p, grid, pa, (int)lds, stream);
+  }
+}
+
 template <int FMT>
 int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
   if (p.n_mtiles == 0) {
-    // decode path: one workgroup per unit (group, 32-row tile pair)
-    constexpr int kT = 2;
-    const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
-    if (grid > 0x7FFFFFFF) return -1;
-    // chunks of 128 k per wave: enough to cover K in one round where possible
-    const int64_t per_wave = ((p.K + 127) / 128 + kDecodeWaves - 1) / kDecodeWaves;
-    if (per_wave <= 2)
-      hipLaunchKernelGGL((k_decode_fwd<FMT, 2, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-    else if (per_wave <= 4)
-      hipLaunchKernelGGL((k_decode_fwd<FMT, 4, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL((k_decode_fwd<FMT, 6, kT>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    const int rc = launch_decode<FMT>(p, stream);
+    if (rc) return rc;
   } else {
     const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kBN - 1) / kBN);
     const int64_t grid = clamp_grid(tiles, cus);
@@ -804,6 +928,9 @@ int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const
   p.t_group = t_group;
   p.n_mtiles = n_mtiles;
   p.G = G;
+  // decode path: block_m carries the largest group size (0: one row each)
+  p.max_m = n_mtiles == 0 ? (block_m > 0 ? block_m : 1) : block_m;
+  if (n_mtiles == 0 && (p.max_m > 16 || (!row_off && p.max_m != 1))) return -1;
   p.N = N;
   p.K = K;
   p.out = static_cast<uint16_t*>(out);

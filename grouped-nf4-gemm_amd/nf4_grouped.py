@@ -414,7 +414,8 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
             r_ptr = r_h.data_ptr()
             keep = (e_h, r_h)
         eids = eids_dev if eids_dev is not None else e_h
-        args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, 0)
+        # decode path: block_m carries the largest group size
+        args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, max_m)
     else:
         bm = _kernel_block_m(block_m if block_m is not None else _prefill_block_m(max_m))
         t0, tr, tg = _tiles_host(sizes_i, bm)

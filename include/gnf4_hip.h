@@ -22,7 +22,9 @@
  *                    guarantees it); `row_off` [G + 1] int32 gives each
  *                    group's rows, or is NULL when every group is exactly
  *                    one row (group g is row g, as in the reference's
- *                    decode grid); the tile table is ignored.
+ *                    decode grid); the tile table is ignored and block_m
+ *                    carries the largest group size (0 or 1 with a NULL
+ *                    row_off; at most 16).
  *   n_mtiles  > 0 -> tiled path: the tile table t_row0/t_rows/t_group
  *                    [n_mtiles] int32 (reference build_group_tiles,
  *                    kernel/nf4_grouped.py:334-362) with block_m in

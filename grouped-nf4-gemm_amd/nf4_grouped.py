@@ -381,6 +381,66 @@ def _stream_ptr(dev) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+class GroupPlan:
+    """Device-resident group tables for repeated calls with the same routing
+    (e.g. inside a captured graph or a timing loop): the expert ids, row
+    offsets or tile table are uploaded once, so a planned call launches the
+    kernel with no host-to-device copy. Not part of the reference's API."""
+
+    def __init__(self, sizes, expert_ids, device, block_m=None):
+        sizes_i = [int(m) for m in sizes]
+        self.G = len(sizes_i)
+        self.max_m = max(sizes_i) if sizes_i else 0
+        self.one_row_each = bool(sizes_i) and min(sizes_i) == 1 and self.max_m == 1
+        dev = torch.device(device)
+        ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else list(expert_ids)
+        self.decode = self.max_m <= DECODE_MAX_ROWS and block_m is None
+        if self.decode:
+            row_off = [0]
+            for m in sizes_i:
+                row_off.append(row_off[-1] + m)
+            self.eids, self.row_off = (torch.tensor(ids, dtype=torch.int32, device=dev),
+                                       torch.tensor(row_off, dtype=torch.int32, device=dev))
+            self.tables = None
+            self.block_m = self.max_m
+        else:
+            self.block_m = _kernel_block_m(block_m if block_m is not None
+                                           else _prefill_block_m(self.max_m))
+            t0, tr, tg = _tiles_host(sizes_i, self.block_m)
+            self.eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+            self.row_off = None
+            self.tables = tuple(torch.tensor(v, dtype=torch.int32, device=dev) for v in (t0, tr, tg))
+        self.n_mtiles = 0 if self.decode else self.tables[0].numel()
+
+    def args(self):
+        if self.decode:
+            ro = None if self.one_row_each else self.row_off.data_ptr()
+            return (self.eids.data_ptr(), ro, self.G, None, None, None, 0, self.max_m)
+        t0, tr, tg = self.tables
+        return (self.eids.data_ptr(), None, self.G, t0.data_ptr(), tr.data_ptr(), tg.data_ptr(),
+                self.n_mtiles, self.block_m)
+
+
+def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
+    """Forward launch with a prepared GroupPlan: the kernel and nothing else."""
+    lib = _hiplib.load()
+    E, N, half = W.shape
+    T, K = a_cat.shape
+    dev = a_cat.device
+    if a_cat.dtype != torch.bfloat16:
+        raise TypeError(f"launch_planned: activations must be bfloat16, got {a_cat.dtype}")
+    a_cat, W, S = _act_view(a_cat), _aligned_rows(W, 16), _scales_view(S)
+    if out is None:
+        out = torch.empty(T, N, dtype=torch.bfloat16, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.gnf4_hip_grouped_fwd(
+            fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+            W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+            *plan.args(), N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    _hiplib.check(rc, "launch_planned")
+    return out
+
+
 def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     """Shared forward launcher for NF4 and MXFP4."""
     lib = _hiplib.load()

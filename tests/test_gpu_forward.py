@@ -292,3 +292,37 @@ def test_mxfp4_e8m0_edges_follow_exp2_multiply():
     assert out[0, 0].item() == 1.0
     assert out[0, 2].item() == 8.0
     assert out[0, 1].item() in (2.0 ** -127, 0.0)   # subnormal kept or flushed
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_planned_launch_matches_the_op_and_replays_in_a_graph(fmt):
+    """GroupPlan + launch_planned (device-resident group tables) give the op's
+    bits, also when captured in a graph and replayed with eager work between."""
+    from nf4_grouped import GroupPlan, launch_planned
+    code = 0 if fmt == "nf4" else 1
+    W, S = _stack(fmt, 16, 512, 1024)
+    dev = torch.device("cuda:0")
+    for sizes, ids in (([1] * 8, list(range(8))), ([3, 0, 16, 2], [5, 1, 9, 0]),
+                       ([40, 130, 1], [2, 7, 3])):
+        a = rand_acts(sum(sizes), 1024)
+        ref = _ops()[fmt](a, W, S, sizes, ids)
+        plan = GroupPlan(sizes, ids, dev)
+        assert torch.equal(launch_planned(code, a, W, S, plan), ref)
+        out = torch.empty_like(ref)
+        launch_planned(code, a, W, S, plan, out=out)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            launch_planned(code, a, W, S, plan, out=out)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            launch_planned(code, a, W, S, plan, out=out)
+        for _ in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)

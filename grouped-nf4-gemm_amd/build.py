@@ -19,7 +19,7 @@ ARCH = os.environ.get("GNF4_HIP_ARCH", "gfx950")
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32 for
 # ordinary float code (this build targets boxes where those forms are avoided).
 HIPCC_FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+    "-O3", "-std=c++17", "-ffp-contract=off", "-fPIC", "-shared", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]

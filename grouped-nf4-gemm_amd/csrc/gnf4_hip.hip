@@ -48,6 +48,9 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
+
+#include <type_traits>
 
 #include "../../include/gnf4_hip.h"
 
@@ -115,6 +118,22 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16(const float2* tab, unsigned
   for (int i = 0; i < 4; ++i) {
     const unsigned addr = __builtin_amdgcn_perm(x, lane_off, 0x0C0C0000u | ((4u + i) << 8));
     const float2 p = *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(tab) + addr);
+    r[i] = bf16x2_bits(p.x * s, p.y * s);
+  }
+  return r;
+}
+
+// Same, with the table at an LDS address below 16 MiB whose bits 8..15 are
+// zero: `base_lane` = table address | lane column, and the address of byte b
+// is base_lane with b in bits 8..15 (one v_perm_b32). `lds0` points at LDS
+// address 0.
+__device__ __forceinline__ u32x4_t nf4_dword_to_bf16_at(const char* lds0, unsigned x,
+                                                        unsigned base_lane, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned addr = __builtin_amdgcn_perm(x, base_lane, 0x0C020000u | ((4u + i) << 8));
+    const float2 p = *reinterpret_cast<const float2*>(lds0 + addr);
     r[i] = bf16x2_bits(p.x * s, p.y * s);
   }
   return r;
@@ -598,6 +617,363 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
   }
 }
 
+// ============================================================== prefill ==
+//
+// Tiled forward for groups larger than the decode path takes. Tile: 128 rows
+// of one group x 256 weight rows (n); four waves, wave w owns the 64 weight
+// rows [64 w, 64 w + 64) for all 128 activation rows, so no weight element is
+// decoded twice. K advances in steps of 64.
+//
+//   * weights: each lane loads 8 packed bytes (16 k values) per 16-row
+//     n-subtile and step straight into registers and decodes them into two
+//     MFMA operands (the weights are MFMA operand A, so the accumulator holds
+//     out^T and a lane ends with 4 consecutive output columns of one row);
+//   * activations: a ring of three 16 KiB LDS stages filled by buffer loads
+//     that write LDS directly (no VGPR round trip). A stage holds 128 rows x
+//     64 k; 16-byte slots are swizzled per row (pf_swz) so the 16-byte
+//     operand reads of a wave run at the full 256 B per clock;
+//   * one flat software pipeline over (tile, k-step) pairs of the workgroup's
+//     whole tile list: the loads of step f + 2 are in flight while step f
+//     computes, across tile boundaries;
+//   * tiles: a persistent grid; the tile list (m-tile major, n-tile minor, so
+//     a group's tiles are adjacent) is cut into eight contiguous ranges, one
+//     per XCD (workgroup b runs on XCD b % 8), so the tiles an XCD runs at
+//     the same time share weights and activations in that XCD's L2.
+//
+// Every vector-memory instruction of a step is counted: kPfGroupLoads per
+// step and wave. The waits on the LDS stages are explicit s_waitcnt
+// immediates computed from that count (stores only add to the count, which
+// makes a wait stricter, never looser).
+constexpr int kPfBM = 128;
+constexpr int kPfBN = 256;
+constexpr int kPfBK = 64;
+constexpr int kPfStage = kPfBM * kPfBK * 2; // bytes per LDS stage
+
+// s_waitcnt with vmcnt(n) and lgkmcnt(0), expcnt untouched (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
+}
+
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Values the kernel knows to be wave-uniform but the compiler may not (it
+// would otherwise keep buffer descriptors in VGPRs and loop over lanes).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+template <class T>
+__device__ __forceinline__ void* uniform_ptr(const T* ptr) {
+  const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  return reinterpret_cast<void*>(lo | (hi << 32));
+}
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// LDS slot swizzle of a staged activation row: 16-byte slot s of row m lives
+// at slot s ^ pf_swz(m % 16). Over the 16 rows one operand read touches this
+// spreads the 16-byte pieces across all 64 banks.
+__device__ __forceinline__ int pf_swz(int m16) { return (m16 ^ (m16 >> 3)) & 7; }
+
+struct PfTile {
+  int row0, rows, e, n0;
+};
+
+// Calls fn(integral_constant<I>) for I = 0 .. S - 1 while it returns true.
+template <int I, int S>
+struct StepUnroll {
+  template <class Fn>
+  __device__ __forceinline__ static bool run(Fn& fn) {
+    if (!fn(std::integral_constant<int, I>{})) return false;
+    return StepUnroll<I + 1, S>::run(fn);
+  }
+};
+template <int S>
+struct StepUnroll<S, S> {
+  template <class Fn>
+  __device__ __forceinline__ static bool run(Fn&) { return true; }
+};
+
+template <int FMT, int kS>
+__global__ void __launch_bounds__(512, 2)
+    k_prefill(const FwdArgs p, const int32_t* __restrict__ t_row0,
+              const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
+              const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
+  static_assert(kS == 4, "ring depth: even, and four 16 KiB stages fill the low 64 KiB");
+  constexpr int kWaves = 8;
+  constexpr int kWaveCols = kPfBN / kWaves;          // 32: one 32 x 32 MFMA column block
+  constexpr int kAPieces = kPfStage / 1024 / kWaves; // LDS-direct loads per wave and step
+  constexpr int kRowsPerWave = kPfBM / kWaves;
+  constexpr int kGroupLoads = kAPieces + 2;          // + weights + scale
+  constexpr int kMT = kPfBM / 32;                    // activation subtiles of 32 rows
+  static_assert(kWaveCols == 32, "one weight subtile per wave");
+  // one LDS object per stage, so the compiler can tell the stages apart when
+  // it places the waits for the direct-to-LDS loads
+  __shared__ __attribute__((aligned(16))) char s_a0[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a1[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a2[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a3[kPfStage];
+  // NF4 pair table: dynamic LDS, which follows the 64 KiB of static stages, so
+  // it starts at 0x10000 and the stages keep addresses an instruction's
+  // 16-bit offset field can hold.
+  extern __shared__ __attribute__((aligned(16))) float2 s_tab[];
+  auto stage_of = [&](auto RI) -> char* {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (r == 0) return s_a0;
+    else if constexpr (r == 1) return s_a1;
+    else if constexpr (r == 2) return s_a2;
+    else return s_a3;
+  };
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);
+  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  // table base (0x10000: byte 2) | lane column; nf4_dword_to_bf16_at takes
+  // byte 2 of this register as address byte 2
+  const unsigned tab_base = (unsigned)(uintptr_t)s_tab;
+  const unsigned lane_off = tab_base | (unsigned)(lane & 31) * 8u;
+  const char* lds0 = reinterpret_cast<const char*>(s_tab) - tab_base;
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+
+  // ---- this workgroup's tiles
+  const int n_tiles = (int)((p.N + kPfBN - 1) / kPfBN);
+  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
+  const int nx = gridDim.x >= 8 ? 8 : 1;
+  const int x = (int)(blockIdx.x % nx), slot = (int)(blockIdx.x / nx);
+  const int wpx = (int)((gridDim.x - x + nx - 1) / nx);   // workgroups on this XCD
+  const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
+  const int my_tiles = lo + slot < hi ? (int)((hi - lo - slot + wpx - 1) / wpx) : 0;
+  const int ksteps = (int)((p.K + kPfBK - 1) / kPfBK);
+  const int F = my_tiles * ksteps;
+  if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
+  if (F == 0) return;
+
+  // Tile descriptors come in through scalar loads (counted by lgkmcnt, so
+  // they never disturb the vector-memory counts the stage waits rely on).
+  auto meta = [&](int j) {
+    PfTile t;
+    const int64_t tg = lo + slot + (int64_t)j * wpx;
+    const int mt = (int)(tg / n_tiles);
+    t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
+    t.row0 = t_row0[mt];
+    t.rows = t_rows[mt];
+    t.e = eids[t_group[mt]];
+    return t;
+  };
+
+  // ---- per-lane constants
+  const int64_t lda2 = p.lda * 2;
+  // A stage: wave w fills its kRowsPerWave rows, 8 rows per instruction
+  int a_row[kAPieces], a_slot[kAPieces];
+#pragma unroll
+  for (int i = 0; i < kAPieces; ++i) {
+    a_row[i] = wave * kRowsPerWave + i * 8 + (lane >> 3);
+    a_slot[i] = (lane & 7) ^ pf_swz(a_row[i] & 15);
+  }
+  // MFMA k mapping within a 64-wide step: lane half h covers k [32 h, 32 h + 32),
+  // MFMA kk (0..3) takes k [32 h + 8 kk, +8) -- 16-byte slot 4 h + kk of a row.
+  // Activation operand kk of subtile i: row i * 32 + l32 at i * 4096 + a_off[kk].
+  int a_off[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) a_off[kk] = l32 * 128 + ((4 * h + kk) ^ pf_swz(l32 & 15)) * 16;
+
+  // ---- ring state
+  u32x4_t wreg[kS];      // 16 packed bytes: row n, k [k0 + 32 h, +32)
+  unsigned sreg[kS];     // its absmax (NF4) or e8m0 byte (MXFP4)
+  PfTile ring_t[kS];
+  bool ring_last[kS];
+  f32x16_t acc[kMT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i) acc[i] = f32x16_t{};
+
+  // ---- issue state: the tile the issue pointer is in. Per tile: buffer
+  // resources and per-lane offsets, with rows and columns outside the tile
+  // folded into out-of-range offsets; per step only the k offset (a scalar
+  // soffset) changes. Steps past the end use zero-size resources, so every
+  // step issues the same instructions and the vector-memory counts hold.
+  int iss_j = 0, iss_ks = 0;
+  PfTile iss_t;
+  const char* a_base = nullptr;
+  const uint8_t* b_base = nullptr;
+  const char* s_base = nullptr;
+  int a_bytes = 0, b_bytes = 0, s_bytes = 0;
+  int a_voff[kAPieces], b_voff = 0, s_voff = 0;
+  auto tile_setup = [&](int j) {
+    iss_t = meta(j);
+    a_base = reinterpret_cast<const char*>(p.a + (int64_t)iss_t.row0 * p.lda);
+    a_bytes = (int)((int64_t)iss_t.rows * lda2);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      a_voff[i] = a_row[i] < iss_t.rows ? (int)(a_row[i] * lda2) + a_slot[i] * 16 : kOOB;
+    b_base = p.B + (int64_t)iss_t.e * p.sbe;
+    b_bytes = (int)(p.N * p.sbn);
+    s_base = static_cast<const char*>(p.S) + (int64_t)iss_t.e * p.sse * kScaleBytes;
+    s_bytes = (int)(p.N * p.ssn * kScaleBytes);
+    const int64_t n = iss_t.n0 + wave * kWaveCols + l32;
+    b_voff = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
+    if constexpr (FMT == kNF4) s_voff = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
+    else s_voff = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+  };
+  tile_setup(0);
+
+  auto issue = [&](auto RI, char* stage, bool live) {
+    constexpr int r = decltype(RI)::value;
+    const int k0 = uniform(iss_ks) * kPfBK;
+    live = uniform(live ? 1 : 0) != 0;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a_base), 0, uniform(live ? a_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(stage + (wave * kAPieces + i) * 1024), 16, a_voff[i], k0 * 2, 0, 0);
+    wreg[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, b_voff, k0 >> 1, 0));
+    if constexpr (FMT == kNF4)
+      sreg[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff, (k0 >> 6) * 4, 0);
+    else
+      sreg[r] = __builtin_amdgcn_raw_buffer_load_b8(rs, s_voff, k0 >> 5, 0);
+    ring_t[r] = iss_t;
+    ring_last[r] = iss_ks == ksteps - 1;
+    // advance
+    if (++iss_ks == ksteps) {
+      iss_ks = 0;
+      ++iss_j;
+      if (iss_j < my_tiles) tile_setup(iss_j);
+    }
+  };
+
+  // Decoded weight operands: wf[r % 2] holds step f's (ring slot r)
+  // operands, decoded during step f - 1 (kS is even, so the two buffers
+  // alternate without copies).
+  u32x4_t wf[2][4];
+  auto decode = [&](auto RI) {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (FMT == kNF4) {
+      const float s = __uint_as_float(sreg[r]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+        wf[r & 1][kk] = nf4_dword_to_bf16_at(lds0, wreg[r][kk], lane_off, s);
+    } else {
+      const float s = e8m0_to_f32(sreg[r]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) wf[r & 1][kk] = mx_dword_to_bf16(wreg[r][kk], s);
+    }
+  };
+
+  // MFMAs of step f (slot r) over the first kM activation subtiles. The
+  // weights are operand A, so acc[i] holds out^T: lane (l32, h) gets token
+  // row i * 32 + l32 and columns 8 g + 4 h + (0..3), g = 0..3.
+  auto mma = [&](auto RI, auto MI, const char* stage) {
+    constexpr int r = decltype(RI)::value;
+    constexpr int kM = decltype(MI)::value;
+    // operands of k-slices kk and kk + 1 in flight; the reads for kk + 2 go
+    // out right after kk's MFMAs, so each MFMA's operand has had a full
+    // k-slice of MFMAs to arrive
+    u32x4_t av[2][kM];
+    auto read = [&](int buf, int kk) {
+#pragma unroll
+      for (int i = 0; i < kM; ++i)
+        av[buf][i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk] + i * 4096);
+    };
+    read(0, 0);
+    read(1, 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kM; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[r & 1][kk]),
+                                                          as_bf16x8(av[kk & 1][i]), acc[i], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk + 2 < 4) read(kk & 1, kk + 2);
+    }
+  };
+
+  // The two waves that share a SIMD (w and w + 4) run the step's two halves
+  // in opposite orders -- decode of step f + 1 then MFMAs of step f, or the
+  // reverse -- so while one wave decodes on the VALU the other keeps the
+  // matrix core busy. The order is a template argument of the whole loop
+  // (each wave half runs its own copy), so no step merges two orders.
+  auto mma_decode = [&](auto RI, auto MI, auto DF, const char* stage) {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (decltype(DF)::value) {
+      decode(std::integral_constant<int, (r + 1) % kS>{});
+      __builtin_amdgcn_sched_barrier(0);
+      mma(RI, MI, stage);
+    } else {
+      mma(RI, MI, stage);
+      __builtin_amdgcn_sched_barrier(0);
+      decode(std::integral_constant<int, (r + 1) % kS>{});
+    }
+  };
+
+  auto compute = [&](auto RI, auto DF, const char* stage) {
+    constexpr int r = decltype(RI)::value;
+    const int rows = uniform(ring_t[r].rows);
+    // every tile runs all 4 subtiles (rows past the group are zeros in LDS):
+    // one straight-line step keeps the accumulators in place
+    mma_decode(RI, std::integral_constant<int, 4>{}, DF, stage);
+    if (ring_last[r]) {
+      const PfTile t = ring_t[r];
+      const int n_l = t.n0 + wave * kWaveCols + 4 * h;   // lane's first column
+      uint16_t* o = out + (int64_t)(t.row0 + l32) * p.ldo + n_l;
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if (i * 32 + l32 < rows && n_l + 8 * g < p.N) {
+            uint2 v;
+            v.x = bf16x2_bits(acc[i][4 * g + 0], acc[i][4 * g + 1]);
+            v.y = bf16x2_bits(acc[i][4 * g + 2], acc[i][4 * g + 3]);
+            *reinterpret_cast<uint2*>(o + (int64_t)i * 32 * p.ldo + 8 * g) = v;
+          }
+        }
+        acc[i] = f32x16_t{};
+      }
+    }
+  };
+
+  // Step f: wait for stage f (loads issued after it: the kS - 2 younger
+  // stages), barrier, refill the stage read in step f - 1 with step
+  // f + kS - 1, compute.
+  int f = 0;
+  auto step = [&](auto RI, auto DF) {
+    constexpr int r = decltype(RI)::value;
+    constexpr int rf = (r + kS - 1) % kS;
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<(kS - 2) * kGroupLoads>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}),
+          f + kS - 1 < F);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(RI, DF, stage_of(RI));
+    return ++f < F;
+  };
+
+  issue(std::integral_constant<int, 0>{}, s_a0, true);
+  issue(std::integral_constant<int, 1>{}, s_a1, F > 1);
+  if constexpr (kS > 3) issue(std::integral_constant<int, 2>{}, s_a2, F > 2);
+  if constexpr (FMT == kNF4) __syncthreads();  // pair table complete
+  decode(std::integral_constant<int, 0>{});
+  if (wave < kWaves / 2) {
+    auto st = [&](auto RI) { return step(RI, std::true_type{}); };
+    while (StepUnroll<0, kS>::run(st)) {
+    }
+  } else {
+    auto st = [&](auto RI) { return step(RI, std::false_type{}); };
+    while (StepUnroll<0, kS>::run(st)) {
+    }
+  }
+}
+
 // ================================================================= dgrad ==
 
 struct DgradArgs {
@@ -848,6 +1224,15 @@ int launch_decode(const FwdArgs& p, hipStream_t stream) {
   }
 }
 
+// GNF4_PREFILL=0 selects the simpler tiled kernel (k_gemm_fwd) instead.
+bool prefill_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("GNF4_PREFILL");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <int FMT>
 int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
@@ -856,6 +1241,26 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
     const int rc = launch_decode<FMT>(p, stream);
     if (rc) return rc;
   } else {
+    const bool pf_ok = p.N % 4 == 0 && p.ldo % 4 == 0 && p.K % kPfBK == 0 &&
+                       (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
+                       (int64_t)kPfBM * p.lda * 2 < 0x7FFFFFFF;
+    if (pf_ok && prefill_enabled()) {
+      const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
+      int64_t grid = tiles < cus ? tiles : cus;
+      const int dyn = FMT == kNF4 ? 8 * kPairEntries : 0;
+      static int configured_dev = -1;
+      int dev = 0;
+      if (hipGetDevice(&dev) != hipSuccess) return -2;
+      if (dyn && configured_dev != dev) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_prefill<FMT, 4>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, dyn) != hipSuccess)
+          return -2;
+        configured_dev = dev;
+      }
+      hipLaunchKernelGGL((k_prefill<FMT, 4>), dim3((unsigned)grid), dim3(512), dyn, stream, p,
+                         p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+      return hipGetLastError() == hipSuccess ? 0 : -2;
+    }
     const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kBN - 1) / kBN);
     const int64_t grid = clamp_grid(tiles, cus);
     switch (block_m) {

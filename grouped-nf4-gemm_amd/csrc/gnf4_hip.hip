@@ -974,6 +974,311 @@ __global__ void __launch_bounds__(512, 2)
   }
 }
 
+// ========================================================== tiled dgrad ==
+//
+// out[t, k] = sum_n grad[t, n] W[e][n, k]: the weights are read transposed.
+// Same skeleton as k_prefill -- 128-row tiles of one group x 256 output
+// columns (here: k), a persistent XCD-contiguous tile list, a 4-stage ring of
+// gradient rows filled by direct-to-LDS loads, one flat pipeline over (tile,
+// 64-wide n-step) -- with the weight operand going through LDS:
+//   * per step each thread loads 4 packed rows (n) x 8 columns (k) -- one
+//     dword per row -- decodes them and writes them transposed (k-major, 4
+//     consecutive n per 8-byte write) into a double-buffered bf16 tile of 256
+//     k-rows x 64 n, decoded during the step before the one that reads it;
+//   * wave w reads its 32 k-rows of that tile as MFMA operand A and the
+//     gradient rows from the stage as operand B (32 x 32 x 16 bf16).
+// The NF4 pair table here has 16 lane columns (32 KiB), so stages, weight
+// tiles and table fit the 160 KiB of LDS.
+constexpr int kDgTile = kPfBN;            // output columns (k) per tile
+constexpr int kDgStep = 64;               // n per step
+constexpr int kDgBStage = kDgTile * kDgStep * 2;
+
+// Pair table with 16 columns: entry (byte b, column c) at b * 128 + c * 8.
+__device__ __forceinline__ void init_pair_table16(float2* tab, int lut) {
+  const unsigned b = threadIdx.x & 255;
+  const float hi = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b >> 4) << 2), lut));
+  const float lo = __int_as_float(__builtin_amdgcn_ds_bpermute((int)((b & 15) << 2), lut));
+  const float2 e = make_float2(hi, lo);
+  const int j0 = threadIdx.x < 256 ? 0 : 8;
+  const int nj = blockDim.x > 256 ? 8 : 16;
+  for (int j = 0; j < nj; ++j) tab[b * 16 + ((j0 + j + b) & 15)] = e;
+}
+
+// 8 NF4 elements of a dword through the 16-column table: `reg2` holds the
+// table address << 1 (bits 8..15 zero) | column * 16.
+__device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsigned x,
+                                                         unsigned reg2, float s) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned addr = __builtin_amdgcn_perm(x, reg2, 0x0C020000u | ((4u + i) << 8)) >> 1;
+    const float2 p = *reinterpret_cast<const float2*>(lds0 + addr);
+    r[i] = bf16x2_bits(p.x * s, p.y * s);
+  }
+  return r;
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(512, 2)
+    k_dgrad_tiled(const FwdArgs p, const int32_t* __restrict__ t_row0,
+                  const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
+                  const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
+  constexpr int kS = 4;
+  constexpr int kWaves = 8;
+  constexpr int kAPieces = kPfStage / 1024 / kWaves;
+  constexpr int kRowsPerWave = kPfBM / kWaves;
+  constexpr int kGroupLoads = kAPieces + 5;          // + 4 weight dwords + 1 scale
+  constexpr int kMT = kPfBM / 32;
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+  __shared__ __attribute__((aligned(16))) char s_a0[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a1[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a2[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_a3[kPfStage];
+  __shared__ __attribute__((aligned(16))) char s_b0[kDgBStage];
+  __shared__ __attribute__((aligned(16))) char s_b1[kDgBStage];
+  extern __shared__ __attribute__((aligned(16))) float2 s_tab[];   // NF4: 32 KiB at 0x20000
+  auto stage_of = [&](auto RI) -> char* {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (r == 0) return s_a0;
+    else if constexpr (r == 1) return s_a1;
+    else if constexpr (r == 2) return s_a2;
+    else return s_a3;
+  };
+  auto bbuf_of = [&](auto RI) -> char* {
+    if constexpr ((decltype(RI)::value & 1) == 0) return s_b0;
+    else return s_b1;
+  };
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);
+  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  // decode role: rows 4 rg .. 4 rg + 3 of the step, columns 8 kc .. 8 kc + 7
+  const int rg = lane & 15, kc = wave * 4 + (lane >> 4);
+  const unsigned tab_base = (unsigned)(uintptr_t)s_tab;
+  const unsigned reg2 = (tab_base << 1) | (unsigned)(lane & 15) * 16u;
+  const char* lds0 = reinterpret_cast<const char*>(s_tab) - tab_base;
+
+  // ---- tiles (output columns k in tiles of 256)
+  const int n_tiles = (int)((p.K + kDgTile - 1) / kDgTile);
+  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
+  const int nx = gridDim.x >= 8 ? 8 : 1;
+  const int x = (int)(blockIdx.x % nx), slot = (int)(blockIdx.x / nx);
+  const int wpx = (int)((gridDim.x - x + nx - 1) / nx);
+  const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
+  const int my_tiles = lo + slot < hi ? (int)((hi - lo - slot + wpx - 1) / wpx) : 0;
+  const int ksteps = (int)(p.N / kDgStep);
+  const int F = my_tiles * ksteps;
+  if constexpr (FMT == kNF4) init_pair_table16(s_tab, lut);
+  if (F == 0) return;
+
+  auto meta = [&](int j) {
+    PfTile t;
+    const int64_t tg = lo + slot + (int64_t)j * wpx;
+    const int mt = (int)(tg / n_tiles);
+    t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kDgTile;   // first output column
+    t.row0 = t_row0[mt];
+    t.rows = t_rows[mt];
+    t.e = eids[t_group[mt]];
+    return t;
+  };
+
+  const int64_t lda2 = p.lda * 2;
+  int a_row[kAPieces], a_slot[kAPieces];
+#pragma unroll
+  for (int i = 0; i < kAPieces; ++i) {
+    a_row[i] = wave * kRowsPerWave + i * 8 + (lane >> 3);
+    a_slot[i] = (lane & 7) ^ pf_swz(a_row[i] & 15);
+  }
+  // MFMA kk (0..3) contracts n [16 kk + 8 h, +8): 16-byte slot 2 kk + h of a
+  // row in both the gradient stage and the weight tile.
+  int a_off[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) a_off[kk] = l32 * 128 + ((2 * kk + h) ^ pf_swz(l32 & 15)) * 16;
+  const int b_wave = wave * 32 * 128;
+
+  unsigned wreg[kS][4];
+  // scale of row n0 + lane of the wave's 32 columns (one scale block: the
+  // columns are 32-aligned); threads pick their rows' with ds_bpermute
+  unsigned sreg[kS];
+  PfTile ring_t[kS];
+  bool ring_last[kS];
+  f32x16_t acc[kMT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i) acc[i] = f32x16_t{};
+
+  int iss_j = 0, iss_ks = 0;
+  PfTile iss_t;
+  const char* a_base = nullptr;
+  const uint8_t* b_base = nullptr;
+  const char* s_base = nullptr;
+  int a_bytes = 0, b_bytes = 0, s_bytes = 0;
+  int a_voff[kAPieces], b_voff[4], s_voff = 0;
+  auto tile_setup = [&](int j) {
+    iss_t = meta(j);
+    a_base = reinterpret_cast<const char*>(p.a + (int64_t)iss_t.row0 * p.lda);
+    a_bytes = (int)((int64_t)iss_t.rows * lda2);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      a_voff[i] = a_row[i] < iss_t.rows ? (int)(a_row[i] * lda2) + a_slot[i] * 16 : kOOB;
+    b_base = p.B + (int64_t)iss_t.e * p.sbe;
+    b_bytes = (int)(p.N * p.sbn);
+    s_base = static_cast<const char*>(p.S) + (int64_t)iss_t.e * p.sse * kScaleBytes;
+    s_bytes = (int)(p.N * p.ssn * kScaleBytes);
+    const int64_t c = iss_t.n0 + kc * 8;                 // first output column of the thread
+    const bool ok = c < p.K;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b_voff[i] = ok ? (int)((4 * rg + i) * p.sbn + (c >> 1)) : kOOB;
+    const int64_t cw = iss_t.n0 + wave * 32;             // the wave's first column
+    if constexpr (FMT == kNF4) s_voff = cw < p.K ? (int)((lane * p.ssn + (cw >> 6)) * 4) : kOOB;
+    else s_voff = cw < p.K ? (int)(lane * p.ssn + (cw >> 5)) : kOOB;
+  };
+  tile_setup(0);
+
+  auto issue = [&](auto RI, char* stage, bool live) {
+    constexpr int r = decltype(RI)::value;
+    const int n0 = uniform(iss_ks) * kDgStep;
+    live = uniform(live ? 1 : 0) != 0;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a_base), 0, uniform(live ? a_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(stage + (wave * kAPieces + i) * 1024), 16, a_voff[i], n0 * 2, 0, 0);
+    const int b_soff = uniform((int)(n0 * p.sbn));
+    const int s_soff = uniform((int)(n0 * p.ssn * kScaleBytes));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wreg[r][i] = __builtin_amdgcn_raw_buffer_load_b32(rb, b_voff[i], b_soff, 0);
+    if constexpr (FMT == kNF4) sreg[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff, s_soff, 0);
+    else sreg[r] = __builtin_amdgcn_raw_buffer_load_b8(rs, s_voff, s_soff, 0);
+    ring_t[r] = iss_t;
+    ring_last[r] = iss_ks == ksteps - 1;
+    if (++iss_ks == ksteps) {
+      iss_ks = 0;
+      ++iss_j;
+      if (iss_j < my_tiles) tile_setup(iss_j);
+    }
+  };
+
+  // Decode the weights of ring slot r into weight tile r & 1 (transposed).
+  auto decode = [&](auto RI) {
+    constexpr int r = decltype(RI)::value;
+    char* bb = bbuf_of(RI);
+    u32x4_t rowv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const unsigned sc = (unsigned)__builtin_amdgcn_ds_bpermute((4 * rg + i) * 4, (int)sreg[r]);
+      if constexpr (FMT == kNF4)
+        rowv[i] = nf4_dword_to_bf16_t16(lds0, wreg[r][i], reg2, __uint_as_float(sc));
+      else
+        rowv[i] = mx_dword_to_bf16(wreg[r][i], e8m0_to_f32(sc));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned r0 = rowv[0][j], r1 = rowv[1][j], r2 = rowv[2][j], r3 = rowv[3][j];
+      const unsigned lo01 = __builtin_amdgcn_perm(r1, r0, 0x05040100u);   // k even: rows 0, 1
+      const unsigned lo23 = __builtin_amdgcn_perm(r3, r2, 0x05040100u);
+      const unsigned hi01 = __builtin_amdgcn_perm(r1, r0, 0x07060302u);   // k odd
+      const unsigned hi23 = __builtin_amdgcn_perm(r3, r2, 0x07060302u);
+      const int k_lo = kc * 8 + 2 * j, k_hi = k_lo + 1;
+      *reinterpret_cast<uint2*>(bb + k_lo * 128 + ((rg >> 1) ^ pf_swz(k_lo & 15)) * 16 + (rg & 1) * 8) =
+          make_uint2(lo01, lo23);
+      *reinterpret_cast<uint2*>(bb + k_hi * 128 + ((rg >> 1) ^ pf_swz(k_hi & 15)) * 16 + (rg & 1) * 8) =
+          make_uint2(hi01, hi23);
+    }
+  };
+
+  auto mma = [&](auto RI, const char* stage) {
+    const char* bb = bbuf_of(RI);
+    u32x4_t wv[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) wv[kk] = *reinterpret_cast<const u32x4_t*>(bb + b_wave + a_off[kk]);
+    u32x4_t av[2][kMT];
+    auto read = [&](int buf, int kk) {
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+        av[buf][i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk] + i * 4096);
+    };
+    read(0, 0);
+    read(1, 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kMT; ++i)
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wv[kk]), as_bf16x8(av[kk & 1][i]),
+                                                          acc[i], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk + 2 < 4) read(kk & 1, kk + 2);
+    }
+  };
+
+  auto compute = [&](auto RI, auto DF, const char* stage) {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (decltype(DF)::value) {
+      decode(std::integral_constant<int, (r + 1) % kS>{});
+      __builtin_amdgcn_sched_barrier(0);
+      mma(RI, stage);
+    } else {
+      mma(RI, stage);
+      __builtin_amdgcn_sched_barrier(0);
+      decode(std::integral_constant<int, (r + 1) % kS>{});
+    }
+    if (ring_last[r]) {
+      const PfTile t = ring_t[r];
+      const int rows = uniform(t.rows);
+      const int c_l = t.n0 + wave * 32 + 4 * h;
+      uint16_t* o = out + (int64_t)(t.row0 + l32) * p.ldo + c_l;
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if (i * 32 + l32 < rows && c_l + 8 * g < p.K) {
+            uint2 v;
+            v.x = bf16x2_bits(acc[i][4 * g + 0], acc[i][4 * g + 1]);
+            v.y = bf16x2_bits(acc[i][4 * g + 2], acc[i][4 * g + 3]);
+            *reinterpret_cast<uint2*>(o + (int64_t)i * 32 * p.ldo + 8 * g) = v;
+          }
+        }
+        acc[i] = f32x16_t{};
+      }
+    }
+  };
+
+  int f = 0;
+  auto step = [&](auto RI, auto DF) {
+    constexpr int r = decltype(RI)::value;
+    constexpr int rf = (r + kS - 1) % kS;
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<(kS - 2) * kGroupLoads>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}),
+          f + kS - 1 < F);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(RI, DF, stage_of(RI));
+    return ++f < F;
+  };
+
+  issue(std::integral_constant<int, 0>{}, s_a0, true);
+  issue(std::integral_constant<int, 1>{}, s_a1, F > 1);
+  issue(std::integral_constant<int, 2>{}, s_a2, F > 2);
+  if constexpr (FMT == kNF4) __syncthreads();  // pair table complete
+  decode(std::integral_constant<int, 0>{});
+  if (wave < kWaves / 2) {
+    auto st = [&](auto RI) { return step(RI, std::true_type{}); };
+    while (StepUnroll<0, kS>::run(st)) {
+    }
+  } else {
+    auto st = [&](auto RI) { return step(RI, std::false_type{}); };
+    while (StepUnroll<0, kS>::run(st)) {
+    }
+  }
+}
+
 // ================================================================= dgrad ==
 
 struct DgradArgs {
@@ -1278,6 +1583,39 @@ template <int FMT>
 int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
+  const bool tiled_ok = p.N % kDgStep == 0 && p.ldo % 4 == 0 &&
+                        (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
+                        (int64_t)kPfBM * p.ldg * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF;
+  if (tiled_ok && prefill_enabled()) {
+    FwdArgs f{};
+    f.a = p.g;
+    f.lda = p.ldg;
+    f.B = p.B;
+    f.sbe = p.sbe;
+    f.sbn = p.sbn;
+    f.S = p.S;
+    f.sse = p.sse;
+    f.ssn = p.ssn;
+    f.n_mtiles = p.n_mtiles;
+    f.N = p.N;
+    f.K = p.K;
+    f.ldo = p.ldo;
+    const int64_t tiles = (int64_t)p.n_mtiles * ((p.K + kDgTile - 1) / kDgTile);
+    const int64_t grid = tiles < cus ? tiles : cus;
+    const int dyn = FMT == kNF4 ? 4 * kPairEntries : 0;   // 16-column table: 32 KiB
+    static int configured_dev = -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -2;
+    if (dyn && configured_dev != dev) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dgrad_tiled<FMT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, dyn) != hipSuccess)
+        return -2;
+      configured_dev = dev;
+    }
+    hipLaunchKernelGGL((k_dgrad_tiled<FMT>), dim3((unsigned)grid), dim3(512), dyn, stream, f,
+                       p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+  }
   const int64_t tiles = (int64_t)p.n_mtiles * ((p.K + kDgBK - 1) / kDgBK);
   const int64_t grid = clamp_grid(tiles, cus);
   switch (block_m) {

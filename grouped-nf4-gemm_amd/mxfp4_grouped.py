@@ -100,7 +100,7 @@ def dgrad_mxfp4_grouped(grad_out, blocks, scales, sizes, expert_ids, config=None
     assert sum(int(m) for m in sizes) == T, (sum(int(m) for m in sizes), T)
     _require_gpu(grad_out, "dgrad_mxfp4_grouped",
                  "The CPU-checkable equivalent is grad_out @ dequant_mxfp4(...) per group.")
-    block_m, _bn, block_k, _w = config or _DGRAD_DEFAULT
+    _bm, _bn, block_k, _w = config or _DGRAD_DEFAULT
     why = None
     if grad_out.dtype != torch.bfloat16:
         why = f"grad_out dtype {grad_out.dtype} is not bfloat16"
@@ -117,4 +117,4 @@ def dgrad_mxfp4_grouped(grad_out, blocks, scales, sizes, expert_ids, config=None
     if len(sizes) != len(expert_ids):
         raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
     return _launch_dgrad(_hiplib.FMT_MXFP4, grad_out, blocks, scales, sizes, expert_ids,
-                         int(block_m), "dgrad_mxfp4_grouped")
+                         "dgrad_mxfp4_grouped")

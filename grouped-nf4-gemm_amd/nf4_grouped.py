@@ -495,7 +495,7 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     return out
 
 
-def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, block_m, op):
+def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     lib = _hiplib.load()
     E, N, half = W.shape
     K = half * 2
@@ -508,8 +508,11 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, block_m, op):
     g = _act_view(grad_out)
     W = _aligned_rows(W, 4)
     S = _scales_view(S)
-    bm = _kernel_block_m(block_m)
-    t0, tr, tg = _tiles_host([int(m) for m in sizes], bm)
+    sizes_i = [int(m) for m in sizes]
+    # tile height from the largest group, as in the forward (the kernel's
+    # per-row arithmetic does not depend on it)
+    bm = _kernel_block_m(_prefill_block_m(max(sizes_i)))
+    t0, tr, tg = _tiles_host(sizes_i, bm)
     eids_dev = _eids_device(expert_ids, dev)
     e_h, t0_d, tr_d, tg_d = to_device_i32(([] if eids_dev is not None else expert_ids,
                                            t0, tr, tg), dev)
@@ -643,9 +646,10 @@ def dgrad_4bit_grouped(grad_out, B, absmax, sizes, expert_ids, config=None):
     same ``[E, N, K/2]`` layout as the forward (no transposed copy).
 
     ``config`` = (BLOCK_M, BLOCK_N, BLOCK_K, num_warps): BLOCK_K must divide
-    64 (eligibility); BLOCK_M picks the tile height. The contraction over N
-    runs in fixed ascending 64-wide steps whatever the config, so the output
-    is bitwise independent of it."""
+    64 (eligibility); the other entries steer the reference's Triton schedule
+    and are accepted unused. The kernel's tiles and its fixed ascending
+    64-wide contraction over N do not depend on the config, so the output is
+    bitwise independent of it."""
     E, N, half = B.shape
     K = half * 2
     T = grad_out.shape[0]
@@ -654,7 +658,7 @@ def dgrad_4bit_grouped(grad_out, B, absmax, sizes, expert_ids, config=None):
         grad_out, "dgrad_4bit_grouped",
         "The CPU-checkable equivalent is grad_out @ dequant_ref(packed, absmax, N, K) "
         "per group.")
-    block_m, _block_n, block_k, _warps = config or _DGRAD_DEFAULT
+    _block_m, _block_n, block_k, _warps = config or _DGRAD_DEFAULT
     why = dgrad_eligible(grad_out, B, absmax, block_k)
     if why is not None:
         raise ValueError(
@@ -668,4 +672,4 @@ def dgrad_4bit_grouped(grad_out, B, absmax, sizes, expert_ids, config=None):
     if len(sizes) != len(expert_ids):
         raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
     return _launch_dgrad(_hiplib.FMT_NF4, grad_out, B, absmax, sizes, expert_ids,
-                         int(block_m), "dgrad_4bit_grouped")
+                         "dgrad_4bit_grouped")

@@ -1499,13 +1499,13 @@ int launch_decode_pa(const FwdArgs& p, int64_t grid, int pa, int lds, hipStream_
   }
 }
 
-// Decode launch: one workgroup of eight waves per unit (group, 32 rows).
+// Decode launch: one workgroup of eight waves per unit (group, 16 kT rows).
 // Groups of at most two rows stage their activations in LDS; larger ones load
 // them into registers. NF4 runs at most two chunks per wave per round (its
 // absmax run load covers two), MXFP4 up to four.
-template <int FMT>
-int launch_decode(const FwdArgs& p, hipStream_t stream) {
-  constexpr int kW = 8, kT = 2;
+template <int FMT, int kT>
+int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
+  constexpr int kW = 8;
   const int64_t per_wave = ((p.K + 127) / 128 + kW - 1) / kW;
   const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
   if (grid > 0x7FFFFFFF) return -1;
@@ -1527,6 +1527,14 @@ int launch_decode(const FwdArgs& p, hipStream_t stream) {
       return launch_decode_pa<FMT, 3, kT>(p, grid, pa, (int)lds, stream);
     return launch_decode_pa<FMT, 4, kT>(p, grid, pa, (int)lds, stream);
   }
+}
+
+// Unit height: 32 rows, or 16 for single-row MXFP4 groups (more workgroups
+// for a stream that needs little decode work per byte).
+template <int FMT>
+int launch_decode(const FwdArgs& p, hipStream_t stream) {
+  if (FMT == kMX && p.max_m == 1) return launch_decode_t<FMT, 1>(p, stream);
+  return launch_decode_t<FMT, 2>(p, stream);
 }
 
 // GNF4_PREFILL=0 selects the simpler tiled kernel (k_gemm_fwd) instead.

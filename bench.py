@@ -243,6 +243,22 @@ def cpu_baseline(model, budget_s=10.0, layers=4):
             "ms_per_layer_pass": round(el * 1e3 / reps / L, 3)}
 
 
+def _timed(fn, dev, reps=10):
+    """(graph-replay ms, eager ms) per call of fn: the graph replays the
+    captured launches and group-table copies without the host-side planning,
+    the eager figure is what a Python caller sees per op call."""
+    import torch
+    ms_graph, _ = time_graph(fn, reps, 3, dev)
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    evs[0].record()
+    for _ in range(reps):
+        fn()
+    evs[1].record()
+    torch.cuda.synchronize()
+    return ms_graph, evs[0].elapsed_time(evs[1]) / reps
+
+
 def prefill_tflops(dev, seed=0):
     """Config 4: Qwen3 NF4 prefill, 4096 tokens x top-8 Zipf(1.1) routing."""
     import numpy as np
@@ -257,20 +273,10 @@ def prefill_tflops(dev, seed=0):
     eids = torch.tensor(ids, dtype=torch.int32, device=dev)
     res = {}
     for name, a, Wt, At, N, K in (("gate_up", x, W, A, 1536, 2048), ("down", h, W2, A2, 2048, 768)):
-        for _ in range(3):
-            gemm_4bit_grouped(a, Wt, At, sizes, eids)
-        torch.cuda.synchronize()
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        reps = 10
-        evs[0].record()
-        for _ in range(reps):
-            gemm_4bit_grouped(a, Wt, At, sizes, eids)
-        evs[1].record()
-        torch.cuda.synchronize()
-        ms = evs[0].elapsed_time(evs[1]) / reps
+        ms, eager = _timed(lambda: gemm_4bit_grouped(a, Wt, At, sizes, eids), dev)
         tf = 2.0 * T * N * K / (ms * 1e-3) / 1e12
         res[name] = {"ms": round(ms, 4), "tflops": round(tf, 1),
-                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "eager_op_ms": round(eager, 4)}
     res["rows"] = T
     res["m_min_max"] = [min(sizes), max(sizes)]
     return res
@@ -286,20 +292,10 @@ def dgrad_tflops(dev, seed=0):
     T = sum(sizes)
     go = (torch.randn(T, 2048, device=dev) * 1e-2).to(torch.bfloat16)
     eids = torch.tensor(ids, dtype=torch.int32, device=dev)
-    for _ in range(3):
-        dgrad_4bit_grouped(go, W, A, sizes, eids)
-    torch.cuda.synchronize()
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-    reps = 10
-    evs[0].record()
-    for _ in range(reps):
-        dgrad_4bit_grouped(go, W, A, sizes, eids)
-    evs[1].record()
-    torch.cuda.synchronize()
-    ms = evs[0].elapsed_time(evs[1]) / reps
+    ms, eager = _timed(lambda: dgrad_4bit_grouped(go, W, A, sizes, eids), dev)
     tf = 2.0 * T * 2048 * 768 / (ms * 1e-3) / 1e12
     return {"ms": round(ms, 4), "tflops": round(tf, 1), "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-            "rows": T}
+            "rows": T, "eager_op_ms": round(eager, 4)}
 
 
 def pmc_workload(model):
@@ -349,6 +345,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--mma-workload", action="store_true",
+                    help="for rocprofv3: the prefill (config 4) and dgrad (config 5) "
+                         "measurements only")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="for rocprofv3 --pmc: one 256 MiB device copy (the counter "
                          "calibration), then the gate_up decode kernel of every layer, "
@@ -362,6 +361,10 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.mma_workload:
+        log(f"[bench] prefill {json.dumps(prefill_tflops(dev))}")
+        log(f"[bench] dgrad {json.dumps(dgrad_tflops(dev))}")
+        return
     log(f"[bench] building Qwen3-30B-A3B NF4 decode model: {args.layers} layers, batch {args.batch}")
     model = DecodeModel("nf4", QWEN, args.batch, dev, layers=args.layers)
     if args.pmc_workload:

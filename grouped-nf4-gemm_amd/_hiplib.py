@@ -12,12 +12,13 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
+DTYPE_F32 = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -27,6 +28,7 @@ _I64 = ctypes.c_int64
 SIGNATURES = {
     "gnf4_hip_abi_version": [],
     "gnf4_hip_device_cus": [],
+    "gnf4_hip_activations_to_bf16": [_P, _I, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_fwd": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_nf4_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,

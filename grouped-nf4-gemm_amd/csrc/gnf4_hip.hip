@@ -1636,6 +1636,49 @@ int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+
+// ----------------------------------------------------- activation widening --
+// fp16 / fp32 activations are rounded once to bf16 (nearest-even, the rounding
+// torch's .to(bfloat16) applies) so that every forward kernel keeps a single
+// bf16 operand type; the bf16 weight path keeps the full fp32 exponent range
+// that adversarial absmax values need. One thread converts 8 elements.
+
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;   // NaN: canonical quiet NaN
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <class SrcT>
+__global__ void __launch_bounds__(256) k_widen_to_bf16(const SrcT* __restrict__ src, int64_t ld_src,
+                                                       uint16_t* __restrict__ dst, int64_t ld_dst,
+                                                       int64_t rows, int64_t vec_per_row) {
+  const int64_t total = rows * vec_per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / vec_per_row, c = (i - r * vec_per_row) * 8;
+    float v[8];
+    if constexpr (sizeof(SrcT) == 2) {
+      typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+      const f16x8_t h = *reinterpret_cast<const f16x8_t*>(src + r * ld_src + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (float)h[j];
+    } else {
+      const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(src + r * ld_src + c);
+      const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(src + r * ld_src + c + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = lo[j];
+        v[4 + j] = hi[j];
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16_rne(v[2 * j]) | (f32_to_bf16_rne(v[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4_t*>(dst + r * ld_dst + c) = o;
+  }
+}
+
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace
@@ -1647,6 +1690,30 @@ extern "C" {
 int gnf4_hip_abi_version(void) { return GNF4_HIP_ABI_VERSION; }
 
 int gnf4_hip_device_cus(void) { return device_cus(); }
+
+int gnf4_hip_activations_to_bf16(const void* src, int src_dtype, int64_t rows, int64_t cols,
+                                 int64_t ld_src, void* dst, int64_t ld_dst, void* stream) {
+  if (src_dtype != GNF4_DTYPE_F16 && src_dtype != GNF4_DTYPE_F32) return -1;
+  if (rows < 0 || cols < 0 || cols % 8 || ld_src < cols || ld_dst < cols || ld_src % 8 ||
+      ld_dst % 8)
+    return -1;
+  if (rows == 0 || cols == 0) return 0;
+  if (!src || !dst || !aligned16(src) || !aligned16(dst)) return -1;
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  const int64_t vec = cols / 8, work = (rows * vec + 255) / 256;
+  const int64_t grid = clamp_grid(work, (int64_t)cus * 8);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (src_dtype == GNF4_DTYPE_F16)
+    hipLaunchKernelGGL((k_widen_to_bf16<_Float16>), dim3((unsigned)grid), dim3(256), 0, s,
+                       static_cast<const _Float16*>(src), ld_src, static_cast<uint16_t*>(dst),
+                       ld_dst, rows, vec);
+  else
+    hipLaunchKernelGGL((k_widen_to_bf16<float>), dim3((unsigned)grid), dim3(256), 0, s,
+                       static_cast<const float*>(src), ld_src, static_cast<uint16_t*>(dst),
+                       ld_dst, rows, vec);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
 
 int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,
                          int64_t stride_be, int64_t stride_bn, const void* scales,

@@ -59,7 +59,8 @@ def gemm_mxfp4_grouped(a_cat, blocks, scales, sizes, expert_ids,
                        block_m: int | None = None, prefill_variant: int | None = None):
     """Single-launch grouped MXFP4 GEMM (reference kernel/mxfp4_grouped.py:134-172).
 
-    ``a_cat [T, K]`` bf16 group-sorted; ``blocks [E, N, K//2]`` uint8;
+    ``a_cat [T, K]`` bf16 (fp16 and fp32 are rounded to bf16 first),
+    group-sorted; ``blocks [E, N, K//2]`` uint8;
     ``scales [E, N, K//32]`` uint8 e8m0; ``sizes`` per-group row counts;
     ``expert_ids [G]`` list / CPU tensor / device tensor. Returns ``[T, N]``
     bf16 in the same group order. Groups of <= 16 rows take the decode kernel

@@ -14,7 +14,9 @@ eager-PyTorch fallback. On a non-GPU tensor the ops raise.
 Numerics: every weight is decoded as ``bf16(fp32(NF4[code] * absmax))`` (one
 fp32 rounding, one bf16 rounding -- the same values ``dequant_ref(...)`` gives
 after ``.to(bfloat16)``), products are exact in the bf16 MFMA and accumulate
-in fp32, and each output is rounded to bf16 once. The reference's Triton
+in fp32, and each output is rounded to bf16 once. fp16 and fp32 activations
+are first rounded to bf16 (nearest-even), so their result equals the
+forward of ``a.to(bfloat16)`` bit for bit. The reference's Triton
 mainloop uses TF32 operands instead; the stated bound is the tolerance
 contract (reference docs/TOLERANCE_CONTRACT.md): B-rel <= 2x the bf16
 dequant-then-matmul path against an fp64 reference, and <= 1e-2.
@@ -369,6 +371,31 @@ def _act_view(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+_WIDEN_DTYPES = {torch.float16: _hiplib.DTYPE_F16, torch.float32: _hiplib.DTYPE_F32}
+
+
+def _bf16_activations(a_cat: torch.Tensor, op: str) -> torch.Tensor:
+    """bf16 activations for the forward kernels. fp16 and fp32 inputs (the
+    reference accepts both, kernel/nf4_grouped.py:456-458) are rounded to bf16
+    once, nearest-even, by the library's widening kernel; any other dtype is
+    a TypeError."""
+    if a_cat.dtype == torch.bfloat16:
+        return _act_view(a_cat)
+    code = _WIDEN_DTYPES.get(a_cat.dtype)
+    if code is None:
+        raise TypeError(f"{op}: activations must be bfloat16, float16 or float32, "
+                        f"got {a_cat.dtype}")
+    src = _act_view(a_cat)
+    T, K = src.shape
+    dst = torch.empty(T, K, dtype=torch.bfloat16, device=src.device)
+    with torch.cuda.device(src.device):
+        rc = _hiplib.load().gnf4_hip_activations_to_bf16(
+            src.data_ptr(), code, T, K, src.stride(0), dst.data_ptr(), dst.stride(0),
+            _stream_ptr(src.device))
+    _hiplib.check(rc, op)
+    return dst
+
+
 def _eids_device(expert_ids, dev):
     """Expert ids as int32 on ``dev``: a device tensor passes through; a list
     or host tensor converts once (same values on every path)."""
@@ -427,9 +454,8 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
     E, N, half = W.shape
     T, K = a_cat.shape
     dev = a_cat.device
-    if a_cat.dtype != torch.bfloat16:
-        raise TypeError(f"launch_planned: activations must be bfloat16, got {a_cat.dtype}")
-    a_cat, W, S = _act_view(a_cat), _aligned_rows(W, 16), _scales_view(S)
+    a_cat, W, S = (_bf16_activations(a_cat, "launch_planned"), _aligned_rows(W, 16),
+                   _scales_view(S))
     if out is None:
         out = torch.empty(T, N, dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
@@ -451,9 +477,7 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     G = len(sizes)
     if T == 0 or G == 0:
         return out
-    if a_cat.dtype != torch.bfloat16:
-        raise TypeError(f"{op}: activations must be bfloat16 in this build, got {a_cat.dtype}")
-    a_cat = _act_view(a_cat)
+    a_cat = _bf16_activations(a_cat, op)
     W = _aligned_rows(W, 16)
     S = _scales_view(S)
     sizes_i = [int(m) for m in sizes]
@@ -547,7 +571,8 @@ def gemm_4bit_grouped(
 ):
     """Single-launch grouped NF4 GEMM (reference kernel/nf4_grouped.py:697-907).
 
-    ``a_cat [T, K]`` bf16, group-sorted; ``B [E, N, K//2]`` uint8;
+    ``a_cat [T, K]`` bf16 (fp16 and fp32 are rounded to bf16 first),
+    group-sorted; ``B [E, N, K//2]`` uint8;
     ``absmax [E, N, K//64]`` fp32; ``sizes`` per-group row counts (a list or
     tensor, read only; zero-size groups are allowed); ``expert_ids [G]`` as a
     list, CPU tensor or device tensor (all give identical bits). Returns

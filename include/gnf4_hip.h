@@ -6,7 +6,9 @@
  * Every call is asynchronous and stream-ordered; none allocates or synchronises.
  *
  * Shared conventions (reference docs/KERNEL_CONTRACT.md, kernel/nf4_grouped.py:697-725):
- *   a / grad_out  [T, ld] bf16, rows sorted by group (group g owns rows
+ *   a / grad_out  [T, ld] bf16 (a_dtype / g_dtype GNF4_DTYPE_BF16; fp16
+ *                 and fp32 activations go through
+ *                 gnf4_hip_activations_to_bf16 first), rows sorted by group (group g owns rows
  *                 row_off[g] .. row_off[g+1]); ld % 8 == 0, 16-byte aligned.
  *   B / blocks    [E, N, K/2] uint8, last dimension contiguous; strides in
  *                 BYTES, multiples of 16 (forward) / 4 (dgrad).
@@ -42,13 +44,14 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 1
+#define GNF4_HIP_ABI_VERSION 2
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
 
 #define GNF4_DTYPE_BF16 0
 #define GNF4_DTYPE_F16 1
+#define GNF4_DTYPE_F32 2
 
 /* ABI version of the loaded library (GNF4_HIP_ABI_VERSION). */
 int gnf4_hip_abi_version(void);
@@ -56,6 +59,17 @@ int gnf4_hip_abi_version(void);
 /* Compute units of the current device (0 on error). Replaces the reference's
  * torch-side SM query `_sm_count` (kernel/nf4_grouped.py:581-591). */
 int gnf4_hip_device_cus(void);
+
+/* Round fp16 (src_dtype GNF4_DTYPE_F16) or fp32 (GNF4_DTYPE_F32) activations
+ * [rows, ld_src] to bf16 [rows, ld_dst], nearest-even (NaN -> 0x7FC0), so a
+ * forward call can take them. The reference's kernels accept fp16 and fp32
+ * activations and widen them in-register (kernel/nf4_grouped.py:456-458,
+ * 511; kernel/mxfp4_grouped.py:94; docs/KERNEL_CONTRACT.md:25); here one
+ * bf16 operand type keeps the weights in bf16's fp32-wide exponent range.
+ * cols, ld_src and ld_dst multiples of 8; src and dst 16-byte aligned. */
+int gnf4_hip_activations_to_bf16(const void *src, int src_dtype, int64_t rows,
+                                 int64_t cols, int64_t ld_src, void *dst,
+                                 int64_t ld_dst, void *stream);
 
 /* Grouped forward for either format: out[t, :] = a[t, :] . dequant(W[e(t)])^T,
  * fp32 accumulation, one bf16 rounding per output. Replaces the launches in

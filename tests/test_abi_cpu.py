@@ -21,7 +21,8 @@ def declared_functions():
 def test_header_declares_the_expected_entry_points():
     names = set(declared_functions())
     assert {"gnf4_hip_nf4_fwd", "gnf4_hip_mxfp4_fwd", "gnf4_hip_nf4_dgrad",
-            "gnf4_hip_mxfp4_dgrad", "gnf4_hip_grouped_fwd", "gnf4_hip_grouped_dgrad"} <= names
+            "gnf4_hip_mxfp4_dgrad", "gnf4_hip_grouped_fwd", "gnf4_hip_grouped_dgrad",
+            "gnf4_hip_activations_to_bf16"} <= names
 
 
 def test_library_exports_every_declared_symbol():
@@ -53,7 +54,7 @@ def test_contract_violations_return_minus_one_without_a_device():
     assert _fwd(lib, K=96) == -1            # NF4 needs K % 64 == 0
     assert _fwd(lib, fmt=1, K=48) == -1     # MXFP4 needs K % 32 == 0
     assert _fwd(lib, fmt=7) == -1
-    assert _fwd(lib, a_dtype=1) == -1       # fp16 activations: not in this build
+    assert _fwd(lib, a_dtype=1) == -1       # fp16 is widened first; the forward takes bf16
     assert _fwd(lib, sbn=24) == -1          # weight rows must be 16-byte aligned
     assert _fwd(lib, lda=60) == -1
     assert _fwd(lib, a=None) == -1
@@ -62,3 +63,16 @@ def test_contract_violations_return_minus_one_without_a_device():
                                       None, 1, 32, 32, 96, 128, 96, None) == -1
     assert lib.gnf4_hip_nf4_dgrad(16, 0, 32, 16, 1024, 32, 32, 32, 1, 64, 48, 48, 48, 0,
                                   32, 32, 64, 128, 64, None) == 0     # nothing to do
+
+
+def test_widening_rejects_bad_arguments_without_a_device():
+    lib = _hiplib.load()
+    w = lib.gnf4_hip_activations_to_bf16
+    assert w(16, _hiplib.DTYPE_BF16, 2, 64, 64, 16, 64, None) == -1   # bf16 needs no widening
+    assert w(16, 9, 2, 64, 64, 16, 64, None) == -1
+    assert w(16, _hiplib.DTYPE_F16, 2, 60, 64, 16, 64, None) == -1    # cols % 8
+    assert w(16, _hiplib.DTYPE_F16, 2, 64, 60, 16, 64, None) == -1    # ld_src < cols
+    assert w(16, _hiplib.DTYPE_F32, 2, 64, 68, 16, 64, None) == -1    # ld_src % 8
+    assert w(8, _hiplib.DTYPE_F32, 2, 64, 64, 16, 64, None) == -1     # 16-byte alignment
+    assert w(None, _hiplib.DTYPE_F32, 2, 64, 64, 16, 64, None) == -1
+    assert w(None, _hiplib.DTYPE_F16, 0, 64, 64, None, 64, None) == 0  # nothing to do

@@ -258,3 +258,75 @@ ORACLE_EXPORT int gnf4o_dgrad_grouped(int fmt, const float *g,
     free(row_off);
     return failed ? -2 : 0;
 }
+
+/* ---------------------------------------------------------------- FFN -- */
+
+/* The locked fp32 silu of the fused expert FFN ("gnf4-silu-horner6/1",
+ * reference gnf4_native/cpu_kernels.c:776-822, numpy spec
+ * kernel/cpu_grouped.py:147-179). The op sequence is the contract:
+ *   x > 87 -> x;  x < -87 -> 0;
+ *   t = x * -log2(e);  n = floor(t + 0.5);  f = t - n;
+ *   p = degree-6 Horner in f (mul then add, never fused);
+ *   e = p * 2^n (exponent bits);  silu = x * (1 / (1 + e)). */
+static float silu_locked(float x) {
+    if (x > 87.0f) return x;
+    if (x < -87.0f) return 0.0f;
+    float t = x * -1.442695040888963e0f;
+    float n = floorf(t + 0.5f);
+    float f = t - n;
+    float p = 1.535336188319500e-4f;
+    p = p * f + 1.339887440266574e-3f;
+    p = p * f + 9.618437357674640e-3f;
+    p = p * f + 5.550332471162809e-2f;
+    p = p * f + 2.402264791363012e-1f;
+    p = p * f + 6.931472028550421e-1f;
+    p = p * f + 1.0f;
+    union { uint32_t u; float f32; } sc;
+    sc.u = (uint32_t)((int32_t)n + 127) << 23;
+    float e = p * sc.f32;
+    return x * (1.0f / (1.0f + e));
+}
+
+ORACLE_EXPORT void gnf4o_silu_locked(const float *x, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = silu_locked(x[i]);
+}
+
+/* Fused NF4 expert FFN, spec form (reference kernel/cpu_grouped.py:182-194,
+ * C entry gnf4_gemv_nf4_ffn_grouped, cpu_kernels.c:948-986):
+ *   gu  = gemv(a, W_gu)                [R, 2H]  locked tree
+ *   h   = silu_locked(gu[:, :H]) * gu[:, H:]   (fp32 multiply)
+ *   out = gemv(h, W_dn)                [R, N_dn] locked tree
+ * The fused form and this composition are the same arithmetic, so the two
+ * agree exactly. */
+ORACLE_EXPORT int gnf4o_ffn_grouped(const float *a, const uint8_t *gu_packed,
+                                    const float *gu_absmax, const uint8_t *dn_packed,
+                                    const float *dn_absmax, const int64_t *eids,
+                                    const int32_t *sizes, int G, int64_t E,
+                                    int64_t N_gu, int64_t K, int64_t N_dn,
+                                    float *out, int threads) {
+    if (N_gu <= 0 || N_gu % 2 || (N_gu / 2) % 64 || K % 64 || N_dn <= 0 || G < 0)
+        return -1;
+    int64_t H = N_gu / 2, R = 0;
+    for (int g = 0; g < G; g++) {
+        if (sizes[g] < 0) return -1;
+        R += sizes[g];
+    }
+    float *gu = (float *)malloc(sizeof(float) * (size_t)(R * N_gu + 1));
+    float *h = (float *)malloc(sizeof(float) * (size_t)(R * H + 1));
+    int rc = (gu && h) ? 0 : -2;
+    if (!rc)
+        rc = gnf4o_gemv_grouped(FMT_NF4, a, gu_packed, gu_absmax, eids, sizes, G, E,
+                                N_gu, K, gu, threads);
+    if (!rc) {
+        for (int64_t r = 0; r < R; r++)
+            for (int64_t j = 0; j < H; j++) {
+                float s = silu_locked(gu[r * N_gu + j]);
+                h[r * H + j] = s * gu[r * N_gu + H + j];
+            }
+        rc = gnf4o_gemv_grouped(FMT_NF4, h, dn_packed, dn_absmax, eids, sizes, G, E,
+                                N_dn, H, out, threads);
+    }
+    free(gu);
+    free(h);
+    return rc;
+}

@@ -59,6 +59,11 @@ def oracle_lib():
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.c_int, _P, _P, _P, _P, _P, ctypes.c_int,
                            _I64, _I64, _I64, _P, ctypes.c_int]
+        lib.gnf4o_silu_locked.restype = None
+        lib.gnf4o_silu_locked.argtypes = [_P, _P, _I64]
+        lib.gnf4o_ffn_grouped.restype = ctypes.c_int
+        lib.gnf4o_ffn_grouped.argtypes = [_P, _P, _P, _P, _P, _P, _P, ctypes.c_int,
+                                          _I64, _I64, _I64, _I64, _P, ctypes.c_int]
         lib.gnf4o_nf4_lut.restype = ctypes.POINTER(ctypes.c_float)
         lib.gnf4o_fp4_lut.restype = ctypes.POINTER(ctypes.c_float)
         _lib = lib
@@ -82,6 +87,12 @@ def ref_lib():
                     fn.restype = ctypes.c_int
                     fn.argtypes = [_P, _P, _P, _P, _P, ctypes.c_int, _I64, _I64,
                                    _P, ctypes.c_int]
+                # 13 arguments: the int64 trio needs registered argtypes
+                # (reference gnf4_native/build.py:121-129)
+                lib.gnf4_gemv_nf4_ffn_grouped.restype = ctypes.c_int
+                lib.gnf4_gemv_nf4_ffn_grouped.argtypes = [
+                    _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _I64, _I64, _I64, _P,
+                    ctypes.c_int]
                 _ref, _ref_path = lib, path
                 break
     return _ref
@@ -157,6 +168,58 @@ def ref_dgrad_grouped(g, packed, scales, sizes, expert_ids, *, fmt, threads=0):
             N, half * 2, _ptr(out), threads)
     if rc:
         raise ValueError(f"reference dgrad rejected the call (rc={rc})")
+    return out
+
+
+def silu_locked(x):
+    """The locked fp32 silu (C oracle), elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    oracle_lib().gnf4o_silu_locked(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def _prep_ffn(a, gu_p, gu_a, dn_p, dn_a, sizes, expert_ids):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    gu_p, dn_p = (np.ascontiguousarray(t, dtype=np.uint8) for t in (gu_p, dn_p))
+    gu_a, dn_a = (np.ascontiguousarray(t, dtype=np.float32) for t in (gu_a, dn_a))
+    eids = np.ascontiguousarray(np.asarray(expert_ids, dtype=np.int64))
+    sz = np.ascontiguousarray(np.asarray(sizes, dtype=np.int32))
+    return a, gu_p, gu_a, dn_p, dn_a, eids, sz
+
+
+def ffn_grouped(a, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids, *,
+                threads=0):
+    """Oracle fused NF4 FFN: gemv -> silu_locked(gate) * up -> gemv, fp32."""
+    a, gu_p, gu_a, dn_p, dn_a, eids, sz = _prep_ffn(a, gu_packed, gu_absmax, dn_packed,
+                                                    dn_absmax, sizes, expert_ids)
+    E, n_gu, half = gu_p.shape
+    n_dn = dn_p.shape[1]
+    out = np.empty((a.shape[0], n_dn), dtype=np.float32)
+    rc = oracle_lib().gnf4o_ffn_grouped(
+        _ptr(a), _ptr(gu_p), _ptr(gu_a), _ptr(dn_p), _ptr(dn_a), _ptr(eids), _ptr(sz),
+        len(sz), E, n_gu, half * 2, n_dn, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"gnf4o_ffn_grouped rejected the call (rc={rc})")
+    return out
+
+
+def ref_ffn_grouped(a, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids, *,
+                    threads=0):
+    """The compiled reference's fused FFN (sizes >= 1, G <= 512)."""
+    lib = ref_lib()
+    if lib is None:
+        raise RuntimeError("reference build absent (oracle/_ref)")
+    a, gu_p, gu_a, dn_p, dn_a, eids, sz = _prep_ffn(a, gu_packed, gu_absmax, dn_packed,
+                                                    dn_absmax, sizes, expert_ids)
+    n_gu, half = gu_p.shape[1], gu_p.shape[2]
+    n_dn = dn_p.shape[1]
+    out = np.empty((a.shape[0], n_dn), dtype=np.float32)
+    rc = lib.gnf4_gemv_nf4_ffn_grouped(
+        _ptr(a), _ptr(gu_p), _ptr(gu_a), _ptr(dn_p), _ptr(dn_a), _ptr(eids), _ptr(sz),
+        len(sz), n_gu, half * 2, n_dn, _ptr(out), threads)
+    if rc:
+        raise ValueError(f"reference ffn rejected the call (rc={rc})")
     return out
 
 

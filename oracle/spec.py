@@ -137,6 +137,55 @@ def ordered_dgrad_ref(g32, packed, scales, sizes, expert_ids, *, fmt):
     return out
 
 
+# Horner coefficients of the locked silu, highest degree first, and the
+# clamp (reference kernel/cpu_grouped.py:147-179, gnf4_native/cpu_kernels.c:789-795).
+SILU_HORNER = (1.535336188319500e-4, 1.339887440266574e-3, 9.618437357674640e-3,
+               5.550332471162809e-2, 2.402264791363012e-1, 6.931472028550421e-1, 1.0)
+SILU_CLAMP = 87.0
+
+
+def silu_locked(x):
+    """The fused FFN's fp32 silu as its fixed op sequence, vectorised: every
+    step below is one IEEE fp32 operation per element, in the reference's
+    order (clamp, t = x * -log2(e), n = floor(t + 0.5), f = t - n, Horner with
+    separate multiply and add, e = p * 2^n, 1 / (1 + e), x * that), with the
+    exact tails x (x > 87) and 0 (x < -87)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        xc = np.clip(x, np.float32(-SILU_CLAMP), np.float32(SILU_CLAMP))
+        t = xc * np.float32(-1.442695040888963e0)
+        n = np.floor(t + np.float32(0.5))
+        f = t - n
+        p = np.full_like(f, np.float32(SILU_HORNER[0]))
+        for c in SILU_HORNER[1:]:
+            p = p * f + np.float32(c)
+        two_n = ((n.astype(np.int32) + 127).astype(np.uint32) << 23).view(np.float32)
+        e = p * two_n
+        r = x * (np.float32(1.0) / (np.float32(1.0) + e))
+    r = np.where(x > np.float32(SILU_CLAMP), x, r)
+    return np.where(x < np.float32(-SILU_CLAMP), np.float32(0.0), r).astype(np.float32)
+
+
+def ref_ffn_grouped(a32, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids):
+    """Fused NF4 FFN spec: forward spec -> silu_locked(gate) * up -> forward
+    spec, gate = the first H outputs, up = the last H (reference
+    kernel/cpu_grouped.py:182-194)."""
+    gu = ref_gemv_grouped(a32, gu_packed, gu_absmax, sizes, expert_ids, fmt="nf4")
+    h_dim = gu.shape[1] // 2
+    h = silu_locked(gu[:, :h_dim]) * gu[:, h_dim:]
+    return ref_gemv_grouped(h, dn_packed, dn_absmax, sizes, expert_ids, fmt="nf4")
+
+
+def fp64_ffn(a, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids):
+    """The FFN in float64 with the exact silu x / (1 + exp(-x))."""
+    gu = fp64_forward(a, gu_packed, gu_absmax, sizes, expert_ids, fmt="nf4")
+    h_dim = gu.shape[1] // 2
+    gate = gu[:, :h_dim]
+    with np.errstate(over="ignore"):
+        h = gate / (1.0 + np.exp(-gate)) * gu[:, h_dim:]
+    return fp64_forward(h, dn_packed, dn_absmax, sizes, expert_ids, fmt="nf4")
+
+
 def fp64_forward(a, packed, scales, sizes, expert_ids, *, fmt):
     """out = a @ dequant(W[e]).T per group in float64 (the tolerance
     contract's reference, reference docs/TOLERANCE_CONTRACT.md)."""

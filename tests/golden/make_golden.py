@@ -48,6 +48,32 @@ def mx_stack(seed, rows, weird, k=K, n=N):
     return a, packed, scales
 
 
+FFN_K, FFN_H, FFN_NDN = 128, 64, 24   # gu [E, 2H, K/2], dn [E, NDN, H/2]
+
+
+def ffn_stack(seed, sizes, scale=1.0):
+    """Fused-FFN inputs in the shape of the reference's own FFN tests
+    (kernel/test_cpu_grouped.py:385-403); `scale` inflates the gu absmax so
+    the gate values cross the silu clamps."""
+    g = np.random.default_rng(seed)
+    gu_p = g.integers(0, 256, size=(E, 2 * FFN_H, FFN_K // 2), dtype=np.uint8)
+    gu_a = (g.random(size=(E, 2 * FFN_H, FFN_K // 64), dtype=np.float32) + 0.5) * np.float32(scale)
+    dn_p = g.integers(0, 256, size=(E, FFN_NDN, FFN_H // 2), dtype=np.uint8)
+    dn_a = g.random(size=(E, FFN_NDN, FFN_H // 64), dtype=np.float32) + 0.5
+    a = g.standard_normal((sum(sizes), FFN_K), dtype=np.float32)
+    eids = [int(x) for x in g.permutation(E)[:len(sizes)]]
+    return a, gu_p, gu_a, dn_p, dn_a, list(sizes), eids
+
+
+def ffn_cases():
+    return {
+        "ffn_nf4_groups_1_9_3": ffn_stack(21, (1, 9, 3)),
+        "ffn_nf4_single_rows": ffn_stack(22, (1, 1, 1, 1)),
+        "ffn_nf4_groups_8_8": ffn_stack(23, (8, 8)),
+        "ffn_nf4_silu_clamps": ffn_stack(24, (2, 5), scale=40.0),
+    }
+
+
 def main():
     if native.ref_lib() is None:
         raise SystemExit("oracle/_ref is not built (needs the reference tree): make -C oracle")
@@ -84,7 +110,20 @@ def main():
     a8 = rng.standard_normal((32, 1024), dtype=np.float32)
     cases["gemv_nf4_config1_slice"] = ("gemv", "nf4", a8, p8, s8, [4] * 8, list(range(8)))
 
+    only = sys.argv[1] if len(sys.argv) > 1 else ""
+    for name, args in ffn_cases().items():
+        if name.startswith(only):
+            x, gu_p, gu_a, dn_p, dn_a, sizes, eids = args
+            out = native.ref_ffn_grouped(x, gu_p, gu_a, dn_p, dn_a, sizes, eids, threads=1)
+            np.savez_compressed(HERE / f"{name}.npz", op="ffn", fmt="nf4", x=x, gu_packed=gu_p,
+                                gu_absmax=gu_a, dn_packed=dn_p, dn_absmax=dn_a,
+                                sizes=np.asarray(sizes, np.int32),
+                                eids=np.asarray(eids, np.int64), out=out,
+                                ref_build=str(native.ref_path().name))
+            print(name, out.shape)
     for name, (op, fmt, x, p, s, sizes, eids) in cases.items():
+        if not name.startswith(only):
+            continue
         fn = native.ref_gemv_grouped if op == "gemv" else native.ref_dgrad_grouped
         out = fn(x, p, s, sizes, eids, fmt=fmt, threads=1)
         np.savez_compressed(HERE / f"{name}.npz", op=op, fmt=fmt, x=x, packed=p, scales=s,

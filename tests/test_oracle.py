@@ -214,6 +214,12 @@ def test_c_oracle_reproduces_the_reference_golden_vectors(path):
     z = np.load(path)                       # allow_pickle stays False
     op, fmt = str(z["op"]), str(z["fmt"])
     sizes, eids = z["sizes"].tolist(), z["eids"].tolist()
+    if op == "ffn":
+        args = (z["x"], z["gu_packed"], z["gu_absmax"], z["dn_packed"], z["dn_absmax"],
+                sizes, eids)
+        assert np.array_equal(native.ffn_grouped(*args), z["out"])
+        assert np.array_equal(spec.ref_ffn_grouped(*args), z["out"])
+        return
     fn = native.gemv_grouped if op == "gemv" else native.dgrad_grouped
     got = fn(z["x"], z["packed"], z["scales"], sizes, eids, fmt=fmt)
     assert np.array_equal(nanfix(got), nanfix(z["out"]))
@@ -222,7 +228,8 @@ def test_c_oracle_reproduces_the_reference_golden_vectors(path):
 def test_golden_set_is_complete():
     names = {p.stem for p in _golden_cases()}
     assert {"gemv_nf4_fixture", "gemv_mxfp4_weird_scales", "dgrad_nf4_fixture",
-            "dgrad_mxfp4_weird_scales", "gemv_nf4_config1_slice"} <= names
+            "dgrad_mxfp4_weird_scales", "gemv_nf4_config1_slice", "ffn_nf4_groups_1_9_3",
+            "ffn_nf4_single_rows", "ffn_nf4_groups_8_8", "ffn_nf4_silu_clamps"} <= names
 
 
 needs_ref = pytest.mark.skipif(native.ref_lib() is None, reason="oracle/_ref not built here")
@@ -321,3 +328,70 @@ def test_packers_round_trip():
     rel = ((dequant_mxfp4(b, s) - w).norm() / w.norm()).item()
     assert 0.05 < rel < 0.16          # reference README: ~0.12
     assert (s.int() - 127).abs().max().item() <= 127
+
+
+# ------------------------------------------------------- fused FFN (silu) --
+
+def test_silu_locked_tracks_true_silu_and_its_tails():
+    """The locked sequence is silu: within 2e-6 relative of float64
+    x / (1 + exp(-x)) on the clamped domain (the reference's own diagnostic
+    bound, kernel/test_cpu_grouped.py:406-424), exactly x above 87 and exactly
+    0 below -87."""
+    x = np.linspace(-87.0, 87.0, 20011, dtype=np.float32)
+    got = spec.silu_locked(x)
+    want = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-6)) < 2e-6
+    big = np.asarray([87.5, 88.0, 500.0, 1e30, np.inf], dtype=np.float32)
+    assert np.array_equal(spec.silu_locked(big), big)
+    assert np.array_equal(spec.silu_locked(-big), np.zeros_like(big))
+    assert spec.silu_locked(np.float32(0.0)) == 0.0
+
+
+def test_silu_c_oracle_equals_the_numpy_spec_bitwise():
+    rng = np.random.default_rng(3)
+    x = np.concatenate([np.linspace(-100, 100, 100001, dtype=np.float32),
+                        rng.standard_normal(50000).astype(np.float32) * 30,
+                        np.asarray([-87, 87, -86.99999, 86.99999, 1e-30, -1e-30], np.float32)])
+    assert np.array_equal(native.silu_locked(x), spec.silu_locked(x))
+
+
+def test_ffn_oracle_is_the_composition_of_its_parts():
+    """gemv -> silu_locked(gate) * up -> gemv, each part the oracle's own."""
+    a, gu_p, gu_a, dn_p, dn_a, sizes, eids = _ffn_case(31, (4, 7))
+    gu = native.gemv_grouped(a, gu_p, gu_a, sizes, eids, fmt="nf4")
+    h = spec.silu_locked(gu[:, :64]) * gu[:, 64:]
+    dn = native.gemv_grouped(h, dn_p, dn_a, sizes, eids, fmt="nf4")
+    assert np.array_equal(native.ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, eids), dn)
+
+
+def test_ffn_oracle_agrees_with_fp64():
+    a, gu_p, gu_a, dn_p, dn_a, sizes, eids = _ffn_case(32, (3, 6, 2))
+    got = native.ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, eids)
+    want = spec.fp64_ffn(a, gu_p, gu_a, dn_p, dn_a, sizes, eids)
+    assert spec.rel_fro(got, want) < 1e-5
+
+
+def test_ffn_oracle_rejects_bad_shapes():
+    a, gu_p, gu_a, dn_p, dn_a, sizes, eids = _ffn_case(33, (2,))
+    with pytest.raises(ValueError):          # odd gu width
+        native.ffn_grouped(a, gu_p[:, :-1], gu_a[:, :-1], dn_p, dn_a, sizes, eids)
+    with pytest.raises(ValueError):          # H % 64 != 0
+        native.ffn_grouped(a, gu_p[:, :96], gu_a[:, :96], dn_p[:, :, :24], dn_a, sizes, eids)
+
+
+def _ffn_case(seed, sizes, scale=1.0):
+    g = np.random.default_rng(seed)
+    gu_p = g.integers(0, 256, size=(E, 128, 64), dtype=np.uint8)
+    gu_a = (g.random(size=(E, 128, 2), dtype=np.float32) + 0.5) * np.float32(scale)
+    dn_p = g.integers(0, 256, size=(E, 24, 32), dtype=np.uint8)
+    dn_a = g.random(size=(E, 24, 1), dtype=np.float32) + 0.5
+    a = g.standard_normal((sum(sizes), 128), dtype=np.float32)
+    return a, gu_p, gu_a, dn_p, dn_a, list(sizes), [int(x) for x in g.permutation(E)[:len(sizes)]]
+
+
+@needs_ref
+@pytest.mark.parametrize("sizes,scale", [((1, 9, 3), 1.0), ((1, 1, 1, 1), 1.0),
+                                         ((8, 8), 1.0), ((2, 5), 40.0), ((12, 3, 1), 7.0)])
+def test_ffn_oracle_equals_the_compiled_reference_live(sizes, scale):
+    args = _ffn_case(40 + len(sizes), sizes, scale)
+    assert np.array_equal(native.ffn_grouped(*args), native.ref_ffn_grouped(*args))

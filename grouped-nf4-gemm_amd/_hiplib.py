@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -29,6 +29,10 @@ SIGNATURES = {
     "gnf4_hip_abi_version": [],
     "gnf4_hip_device_cus": [],
     "gnf4_hip_activations_to_bf16": [_P, _I, _I64, _I64, _I64, _P, _I64, _P],
+    "gnf4_hip_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
+    "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                             _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
+                             _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_fwd": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_nf4_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,

@@ -257,11 +257,48 @@ __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t
   }
 }
 
-// Decode path. A unit is (group g, kTiles x 16 weight rows). The
-// workgroup's kDecodeWaves waves split the unit's 128-element K chunks into
-// contiguous runs (wave w takes chunks w * kChunksPerWave, ...). Every buffer
-// load costs the CU's vector-memory front end about the same whatever its
-// lane mask, so the kernel keeps their number low:
+// Unit kinds of the decode body.
+//   kPlain   out = a . W^T over the unit's 16 * kTiles rows.
+//   kFfnGu   fused FFN, first stage: tile 0 holds 16 gate rows (n), tile 1
+//            the matching up rows (H + n); the epilogue writes
+//            h = bf16(silu_locked(bf16(gate)) * bf16(up)) instead of gu.
+//   kFfnDn   fused FFN, second stage: a plain unit over h whose weight
+//            loads are issued before it waits for h to be complete.
+constexpr int kPlain = 0, kFfnGu = 1, kFfnDn = 2;
+
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// The locked fp32 silu of the fused FFN: a fixed op sequence, no FMA
+// (this file builds with -ffp-contract=off), IEEE division. Same steps as
+// the reference's gnf4_native/cpu_kernels.c:797-822 ("gnf4-silu-horner6/1").
+__device__ __forceinline__ float silu_locked(float x) {
+  if (x > 87.0f) return x;
+  if (x < -87.0f) return 0.0f;
+  const float t = x * -1.442695040888963e0f;
+  const float n = floorf(t + 0.5f);
+  const float f = t - n;
+  float q = 1.535336188319500e-4f;
+  q = q * f + 1.339887440266574e-3f;
+  q = q * f + 9.618437357674640e-3f;
+  q = q * f + 5.550332471162809e-2f;
+  q = q * f + 2.402264791363012e-1f;
+  q = q * f + 6.931472028550421e-1f;
+  q = q * f + 1.0f;
+  const float e = q * __uint_as_float((uint32_t)((int)n + 127) << 23);
+  return x * (1.0f / (1.0f + e));
+}
+
+__device__ __forceinline__ float bf16_round(float f) {
+  return __uint_as_float((uint32_t)f32_to_bf16_bits(f) << 16);
+}
+
+// One decode unit: (group g, kTiles x 16 weight rows). The workgroup's
+// kDecodeWaves waves split the unit's 128-element K chunks into contiguous
+// runs (wave w takes chunks w * kChunksPerWave, ...). Every buffer load costs
+// the CU's vector-memory front end about the same whatever its lane mask, so
+// the body keeps their number low:
 //   * with kAPieces > 0 (groups of at most two rows) the group's activation
 //     rows are staged once per workgroup into LDS (a few 16-byte loads per
 //     thread) in a [k / 8][row] layout and each MFMA A operand is a 16-byte
@@ -271,25 +308,31 @@ __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t
 //   * each weight load moves 16 bytes per lane (32 elements of one row);
 //   * an NF4 lane's absmax values for a whole run are one 16-byte load;
 // and issues all of them before the first wait. The waves then reduce their
-// 16 x 16 partial tiles through LDS in wave order (deterministic).
+// 16 x 16 partial tiles through LDS in wave order (deterministic). The
+// summation order of an output depends on K only, never on the unit kind or
+// on which tile the row sits in.
 //
 // Dynamic LDS: [NF4 pair table 64 KiB][activations M * K * 2][zero block];
 // the reduction buffer reuses the start once the table is no longer read.
-template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces>
-// two workgroups per CU: kDecodeWaves / 2 waves per SIMD
-__global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_fwd(const FwdArgs p) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
+// `lut` is the lane's codebook register (nf4_lut_lane). `ffn_h` is H for
+// kFfnGu. `wait_acts` runs, in every thread, after the first round's weight
+// loads are issued and before any activation load (kFfnDn).
+template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces, int kKind,
+          class Wait>
+__device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, char* smem,
+                                            const int lut, const int64_t ffn_h,
+                                            const Wait& wait_acts) {
+  static_assert(kKind != kFfnGu || (FMT == kNF4 && kTiles == 2), "gate/up pairs need 2 tiles");
   float2* s_tab = reinterpret_cast<float2*>(smem);
-  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
-  __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
   constexpr int kThreadsD = 64 * kDecodeWaves;
+  constexpr bool kLateActs = kKind == kFfnDn;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nl = lane & 15;
   const int q = lane >> 4;
   const unsigned lane_off = (unsigned)(lane & 31) * 8u;
-  const int64_t n_units = (p.N + 16 * kTiles - 1) / (16 * kTiles);
-  const int64_t u = blockIdx.x;  // one unit per workgroup
+  const int64_t n_units =
+      kKind == kFfnGu ? ffn_h / 16 : (p.N + 16 * kTiles - 1) / (16 * kTiles);
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
 
   const int g = (int)(u / n_units);
@@ -307,14 +350,17 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
   const int pieces = M * kslices;
   u32x4_t av[kAPieces > 0 ? kAPieces : 1];
+  auto stage_loads = [&]() {
 #pragma unroll
-  for (int i = 0; i < kAPieces; ++i) {
-    const int pc = (int)threadIdx.x + i * kThreadsD;
-    if (wave * 64 + i * kThreadsD < pieces) {         // uniform: whole waves skip
-      const int m = pc / kslices, sl = pc - m * kslices;
-      av[i] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+    for (int i = 0; i < kAPieces; ++i) {
+      const int pc = (int)threadIdx.x + i * kThreadsD;
+      if (wave * 64 + i * kThreadsD < pieces) {         // uniform: whole waves skip
+        const int m = pc / kslices, sl = pc - m * kslices;
+        av[i] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+      }
     }
-  }
+  };
+  if constexpr (!kLateActs) stage_loads();
 
   // ---- weight and scale loads
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
@@ -323,7 +369,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   int b_row[kTiles], s_row[kTiles];
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
-    const int64_t n = (nu * kTiles + t) * 16 + nl;
+    const int64_t n = kKind == kFfnGu ? t * ffn_h + nu * 16 + nl : (nu * kTiles + t) * 16 + nl;
     b_row[t] = n < p.N ? (int)(n * p.sbn) : kOOB;
     s_row[t] = n < p.N ? (int)(n * p.ssn * kScaleBytes) : kOOB;
   }
@@ -337,7 +383,9 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   // first; in the first round the LDS staging (table, activations) happens
   // while they are in flight.
   static_assert(FMT != kNF4 || kChunksPerWave <= 2, "one 16-byte absmax load per run");
-  auto round = [&](int c0, bool first) {
+  auto round = [&](int c0, auto first_tag) {
+    constexpr bool first = decltype(first_tag)::value;
+    constexpr bool late = kLateActs && first;  // activations after the wait
     u32x4_t wb[kChunksPerWave][kTiles];
     unsigned sb[kChunksPerWave][kTiles];
     u32x4_t sv[kTiles];
@@ -352,6 +400,16 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
         sv[t] = buf_load16(rs, soff);
       }
     }
+    auto act_loads = [&](int i) {
+      if constexpr (kAPieces == 0) {
+        const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+        const bool kval = kseg < (unsigned)K32;
+        // rows >= M fall outside the activation resource and load as zeros
+        const int aoff = oob_unless(kval, (int)((int64_t)nl * p.lda * 2) + (int)kseg * 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
+      }
+    };
 #pragma unroll
     for (int i = 0; i < kChunksPerWave; ++i) {
       const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
@@ -362,12 +420,13 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
         if constexpr (FMT != kNF4)
           sb[i][t] = buf_load1(rs, oob_unless(kval, s_row[t] + (int)(kseg >> 5)));
       }
-      if constexpr (kAPieces == 0) {
-        // rows >= M fall outside the activation resource and load as zeros
-        const int aoff = oob_unless(kval, (int)((int64_t)nl * p.lda * 2) + (int)kseg * 2);
+      if constexpr (!late) act_loads(i);
+    }
+    if constexpr (late) {
+      wait_acts();
+      stage_loads();
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
-      }
+      for (int i = 0; i < kChunksPerWave; ++i) act_loads(i);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the load block ahead of all use
     if constexpr (FMT == kNF4) {
@@ -379,7 +438,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
           sb[i][t] = idx == 0 ? sv[t][0] : idx == 1 ? sv[t][1] : idx == 2 ? sv[t][2] : sv[t][3];
         }
     }
-    if (first) {
+    if constexpr (first) {
       if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
       if (kAPieces > 0 && threadIdx.x < 4)
         *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
@@ -426,30 +485,170 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
       }
     }
   };
-  round(wave * kChunksPerWave, true);  // every wave runs it: chunks past the end load zeros
+  // every wave runs the first round: chunks past the end load zeros
+  round(wave * kChunksPerWave, std::true_type{});
   for (int c0 = (kDecodeWaves + wave) * kChunksPerWave; c0 < nchunks;
        c0 += kDecodeWaves * kChunksPerWave)
-    round(c0, false);
+    round(c0, std::false_type{});
 
   __syncthreads();  // the table is no longer read: its space takes the partials
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem);   // [kDecodeWaves][kTiles][64]
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) s_red[(wave * kTiles + t) * 64 + lane] = acc[t][0] + acc[t][1];
   __syncthreads();
-  // wave t < kTiles sums tile t over the waves in wave order (deterministic)
-  if (wave < kTiles) {
-    const int t = wave;
-    const int64_t n = (nu * kTiles + t) * 16 + nl;
-    f32x4_t v = s_red[t * 64 + lane];
+  if constexpr (kKind == kFfnGu) {
+    // wave 0 sums the gate and up tiles over the waves in wave order and
+    // writes h for its 16 columns: the same bits as a plain gu launch
+    // (bf16 out) followed by the silu-multiply kernel
+    if (wave == 0) {
+      f32x4_t vg = s_red[lane], vu = s_red[64 + lane];
 #pragma unroll
-    for (int w = 1; w < kDecodeWaves; ++w) v = v + s_red[(w * kTiles + t) * 64 + lane];
-    if (n < p.N) {
+      for (int w = 1; w < kDecodeWaves; ++w) {
+        vg = vg + s_red[(w * kTiles) * 64 + lane];
+        vu = vu + s_red[(w * kTiles + 1) * 64 + lane];
+      }
+      const int64_t col = nu * 16 + nl;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 4 * q + i;
-        if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+        if (m < M) {
+          const float hv = silu_locked(bf16_round(vg[i])) * bf16_round(vu[i]);
+          p.out[(int64_t)(r0 + m) * p.ldo + col] = f32_to_bf16_bits(hv);
+        }
       }
     }
+  } else {
+    // wave t < kTiles sums tile t over the waves in wave order (deterministic)
+    if (wave < kTiles) {
+      const int t = wave;
+      const int64_t n = (nu * kTiles + t) * 16 + nl;
+      f32x4_t v = s_red[t * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < kDecodeWaves; ++w) v = v + s_red[(w * kTiles + t) * 64 + lane];
+      if (n < p.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * q + i;
+          if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+        }
+      }
+    }
+  }
+}
+
+// Decode path: one unit per workgroup.
+template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces>
+// two workgroups per CU: kDecodeWaves / 2 waves per SIMD
+__global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_fwd(const FwdArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
+  decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain>(
+      p, (int64_t)blockIdx.x, smem, lut, 0, NoWait{});
+}
+
+// ------------------------------------------------------------ fused FFN --
+//
+// gate_up -> silu(gate) * up -> down for groups of at most 16 rows, in one
+// launch. Units are numbered by a ticket taken when a workgroup starts, so
+// numbers are handed out in start order: the G * (H / 16) gate/up units come
+// first, then the G * ceil(N_dn / 32) down units. A gate/up unit writes its
+// 16 columns of h (bf16, [T, ldh]) and then bumps its group's counter with
+// release semantics; a down unit issues its weight loads, waits until its
+// group's counter shows every gate/up unit of the group (acquire), and then
+// reads h. A down unit only ever waits on units with smaller tickets, which
+// are running or done, so the wait always ends.
+//
+// Sync words (u32, device memory, zero before the first call): [0] ticket,
+// [1] error flag, [2 + 2g] group g's arrivals, [3 + 2g] its departures.
+// Every word is back at zero when a call ends: the workgroup that takes the
+// last ticket subtracts the call's ticket count, and the last down unit of a
+// group to pass its wait clears that group's pair. Stream-ordered calls can
+// therefore share one sync buffer; calls that overlap on it race.
+constexpr int kFfnSpinLimit = 1 << 22;   // polls before a down unit gives up
+constexpr int kFfnMaxDynLds = 159 * 1024; // dynamic LDS beside the static ticket word
+
+template <int CPW1, int CPW2, int kAPieces>
+__global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const FwdArgs dn,
+                                                       const int64_t H, uint32_t* sync,
+                                                       const uint32_t n_tickets) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  __shared__ uint32_t s_ticket;
+  if (threadIdx.x == 0) {
+    const uint32_t t =
+        __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == n_tickets - 1)   // every ticket of this call is taken
+      __hip_atomic_fetch_add(sync, 0u - n_tickets, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ticket = t;
+  }
+  __syncthreads();
+  const int64_t u = (int64_t)s_ticket;
+  const int lut = nf4_lut_lane();
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t gu_per_group = H / 16;
+  const int64_t gu_units = (int64_t)gu.G * gu_per_group;
+  if (u < gu_units) {
+    const int g = (int)(u / gu_per_group);
+    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, u, smem, lut, H, NoWait{});
+    const int M = gu.row_off ? gu.row_off[g + 1] - gu.row_off[g] : 1;
+    if (M <= 0) return;                 // empty group: nobody waits on it
+    // every thread's h stores are complete and visible at agent scope
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      __hip_atomic_fetch_add(sync + 2 + 2 * g, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  const int64_t dn_per_group = (dn.N + 31) / 32;
+  const int64_t u2 = u - gu_units;
+  const int g = (int)(u2 / dn_per_group);
+  auto wait_h = [&]() {
+    if (threadIdx.x == 0) {
+      uint32_t* arrived = sync + 2 + 2 * g;
+      int spins = 0;
+      while (__hip_atomic_load(arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             (uint32_t)gu_per_group) {
+        if (++spins > kFfnSpinLimit) {   // not expected: flag it and go on
+          __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      // the group's last unit past this point clears its pair for the next call
+      if (__hip_atomic_fetch_add(sync + 3 + 2 * g, 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)dn_per_group - 1) {
+        __hip_atomic_store(arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sync + 3 + 2 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  };
+  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, u2, smem, lut, 0, wait_h);
+}
+
+// Elementwise silu-multiply for the unfused path (and groups too large for
+// the fused decode kernel): h[t, j] = bf16(silu_locked(gu[t, j]) * gu[t, H + j]),
+// gu bf16 [T, ldg], h bf16 [T, ldh]. Eight columns per thread.
+__global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ gu, int64_t ldg,
+                                                  uint16_t* __restrict__ h, int64_t ldh,
+                                                  int64_t T, int64_t H) {
+  const int64_t vec = H / 8, total = T * vec;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / vec, c = (i - t * vec) * 8;
+    const u32x4_t gv = *reinterpret_cast<const u32x4_t*>(gu + t * ldg + c);
+    const u32x4_t uv = *reinterpret_cast<const u32x4_t*>(gu + t * ldg + H + c);
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float g0 = __uint_as_float(gv[j] << 16), g1 = __uint_as_float(gv[j] & 0xFFFF0000u);
+      const float u0 = __uint_as_float(uv[j] << 16), u1 = __uint_as_float(uv[j] & 0xFFFF0000u);
+      o[j] = (uint32_t)f32_to_bf16_bits(silu_locked(g0) * u0) |
+             ((uint32_t)f32_to_bf16_bits(silu_locked(g1) * u1) << 16);
+    }
+    *reinterpret_cast<u32x4_t*>(h + t * ldh + c) = o;
   }
 }
 
@@ -1509,7 +1708,8 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   const int64_t per_wave = ((p.K + 127) / 128 + kW - 1) / kW;
   const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
   if (grid > 0x7FFFFFFF) return -1;
-  const bool stage = p.max_m <= 2;
+  // LDS staging covers at most 4 pieces of 16 bytes per thread
+  const bool stage = p.max_m <= 2 && (int64_t)p.max_m * p.K * 2 <= 4 * 64 * kW * 16;
   const int64_t a_bytes = stage ? (int64_t)p.max_m * p.K * 2 : 0;
   const int64_t pieces = (a_bytes + 15) / 16;
   const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
@@ -1535,6 +1735,61 @@ template <int FMT>
 int launch_decode(const FwdArgs& p, hipStream_t stream) {
   if (FMT == kMX && p.max_m == 1) return launch_decode_t<FMT, 1>(p, stream);
   return launch_decode_t<FMT, 2>(p, stream);
+}
+
+// Fused FFN decode launch (every group at most 16 rows). Phase shapes:
+// gate/up over K, down over H; the chunk split per wave follows each K.
+template <int CPW1, int CPW2, int PA>
+int launch_ffn_inst(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
+                    uint32_t n_tickets, int lds, hipStream_t stream) {
+  static int configured_dev = -1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  if (configured_dev != dev) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ffn_decode<CPW1, CPW2, PA>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kFfnMaxDynLds) !=
+        hipSuccess)
+      return -2;
+    configured_dev = dev;
+  }
+  hipLaunchKernelGGL((k_ffn_decode<CPW1, CPW2, PA>), dim3(n_tickets), dim3(512), lds, stream,
+                     gu, dn, H, sync, n_tickets);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+template <int CPW1, int CPW2>
+int launch_ffn_pa(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
+                  uint32_t n_tickets, int pa, int lds, hipStream_t stream) {
+  switch (pa) {
+    case 1: return launch_ffn_inst<CPW1, CPW2, 1>(gu, dn, H, sync, n_tickets, lds, stream);
+    case 2: return launch_ffn_inst<CPW1, CPW2, 2>(gu, dn, H, sync, n_tickets, lds, stream);
+    case 4: return launch_ffn_inst<CPW1, CPW2, 4>(gu, dn, H, sync, n_tickets, lds, stream);
+    default: return launch_ffn_inst<CPW1, CPW2, 0>(gu, dn, H, sync, n_tickets, lds, stream);
+  }
+}
+
+int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
+               hipStream_t stream) {
+  constexpr int kW = 8;
+  const int64_t tickets = (int64_t)gu.G * (H / 16) + (int64_t)gu.G * ((dn.N + 31) / 32);
+  if (tickets <= 0) return 0;
+  if (tickets > 0x7FFFFFFF) return -1;
+  const int64_t kmax = gu.K > dn.K ? gu.K : dn.K;
+  const bool stage = gu.max_m <= 2 && (int64_t)gu.max_m * kmax * 2 <= 4 * 64 * kW * 16;
+  const int64_t a_bytes = stage ? (int64_t)gu.max_m * kmax * 2 : 0;
+  const int64_t pieces = (a_bytes + 15) / 16;
+  const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
+  int64_t lds = 8 * kPairEntries + ((a_bytes + 15) & ~15) + 64;
+  const int64_t red = (int64_t)kW * 2 * 64 * 16;
+  if (lds < red) lds = red;
+  if (lds > kFfnMaxDynLds) return -1;
+  const bool two1 = ((gu.K + 127) / 128 + kW - 1) / kW > 1;
+  const bool two2 = ((dn.K + 127) / 128 + kW - 1) / kW > 1;
+  const uint32_t n = (uint32_t)tickets;
+  if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
+  if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, sync, n, pa, (int)lds, stream);
+  if (two2) return launch_ffn_pa<1, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
+  return launch_ffn_pa<1, 1>(gu, dn, H, sync, n, pa, (int)lds, stream);
 }
 
 // GNF4_PREFILL=0 selects the simpler tiled kernel (k_gemm_fwd) instead.
@@ -1713,6 +1968,78 @@ int gnf4_hip_activations_to_bf16(const void* src, int src_dtype, int64_t rows, i
                        static_cast<const float*>(src), ld_src, static_cast<uint16_t*>(dst),
                        ld_dst, rows, vec);
   return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_silu_mul(const void* gu, int64_t ldg, int64_t T, int64_t H, void* h, int64_t ldh,
+                      void* stream) {
+  if (T < 0 || H <= 0 || H % 8 || ldg < 2 * H || ldg % 8 || ldh < H || ldh % 8) return -1;
+  if (T == 0) return 0;
+  if (!gu || !h || !aligned16(gu) || !aligned16(h)) return -1;
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  const int64_t work = (T * (H / 8) + 255) / 256;
+  const int64_t grid = clamp_grid(work, (int64_t)cus * 8);
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gu), ldg,
+                     static_cast<uint16_t*>(h), ldh, T, H);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* B_gu,
+                         int64_t gu_sbe, int64_t gu_sbn, const float* absmax_gu,
+                         int64_t gu_sae, int64_t gu_san, const uint8_t* B_dn, int64_t dn_sbe,
+                         int64_t dn_sbn, const float* absmax_dn, int64_t dn_sae,
+                         int64_t dn_san, const int32_t* expert_ids, const int32_t* row_off,
+                         int G, int max_m, int64_t N_gu, int64_t K, int64_t N_dn, void* h,
+                         int64_t ldh, uint32_t* sync, int64_t sync_words, void* out,
+                         int64_t ldo, void* stream) {
+  if (a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N_gu <= 0 || N_gu % 2 || (N_gu / 2) % 64 || K <= 0 || K % 64 || N_dn <= 0 || G < 0)
+    return -1;
+  const int64_t H = N_gu / 2;
+  if (max_m < 1 || max_m > 16 || (!row_off && max_m != 1)) return -1;
+  if (!a || !B_gu || !absmax_gu || !B_dn || !absmax_dn || !expert_ids || !h || !sync || !out)
+    return -1;
+  if (lda < K || lda % 8 || ldh < H || ldh % 8 || ldo < N_dn || !aligned16(a) || !aligned16(h))
+    return -1;
+  if (gu_sbn % 16 || gu_sbe % 16 || dn_sbn % 16 || dn_sbe % 16 || !aligned16(B_gu) ||
+      !aligned16(B_dn))
+    return -1;
+  if (sync_words < 2 + 2 * (int64_t)G || ((reinterpret_cast<uintptr_t>(sync) & 3) != 0))
+    return -1;
+  if (G == 0) return 0;
+  FwdArgs gu{};
+  gu.a = static_cast<const uint16_t*>(a);
+  gu.lda = lda;
+  gu.B = B_gu;
+  gu.sbe = gu_sbe;
+  gu.sbn = gu_sbn;
+  gu.S = absmax_gu;
+  gu.sse = gu_sae;
+  gu.ssn = gu_san;
+  gu.eids = expert_ids;
+  gu.row_off = row_off;
+  gu.G = G;
+  gu.max_m = max_m;
+  gu.N = N_gu;
+  gu.K = K;
+  gu.out = static_cast<uint16_t*>(h);
+  gu.ldo = ldh;
+  FwdArgs dn = gu;
+  dn.a = static_cast<const uint16_t*>(h);
+  dn.lda = ldh;
+  dn.B = B_dn;
+  dn.sbe = dn_sbe;
+  dn.sbn = dn_sbn;
+  dn.S = absmax_dn;
+  dn.sse = dn_sae;
+  dn.ssn = dn_san;
+  dn.N = N_dn;
+  dn.K = H;
+  dn.out = static_cast<uint16_t*>(out);
+  dn.ldo = ldo;
+  if (device_cus() <= 0) return -2;
+  return launch_ffn(gu, dn, H, sync, static_cast<hipStream_t>(stream));
 }
 
 int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,

@@ -1,0 +1,179 @@
+"""Grouped NF4 expert FFN on MI355X: gate_up -> silu(gate) * up -> down.
+
+``gemm_nf4_ffn_grouped`` is the GPU form of the reference's fused CPU FFN
+(``gemm_nf4_ffn_grouped_cpu``, kernel/cpu_grouped.py:288-346; C entry
+gnf4_native/cpu_kernels.c:948-986), which the reference has only for its CPU
+tier. Layouts and error behaviour follow that wrapper:
+``gu_packed [E, 2H, K/2]`` u8 + ``gu_absmax [E, 2H, K/64]`` f32 (gate = the
+first H outputs, up = the last H), ``dn_packed [E, N_dn, H/2]`` u8 +
+``dn_absmax [E, N_dn, H/64]`` f32, ``H % 64 == 0``.
+
+Two paths, both HIP:
+  * every group at most 16 rows (decode): ONE launch of the fused kernel.
+    gate/up units write the intermediate h straight from their epilogue and
+    signal a per-group counter; down units stream their weights meanwhile
+    and start the moment their group's h is complete. No gu tensor is
+    written, and there is no second or third launch.
+  * larger groups: the tiled forward kernel for gate_up, the silu-multiply
+    kernel, the tiled forward kernel for down.
+
+Numerics: gate and up are the bf16 outputs of the forward kernel, h is
+``bf16(silu_locked(gate) * up)`` with the reference's locked fp32 silu
+(kernel/cpu_grouped.py:147-179), and the result is bf16. The fused launch
+gives the same bits as the three-launch composition, which is how the tests
+pin it. Against the reference's fp32 CPU FFN the bound is the tolerance
+contract (docs/TOLERANCE_CONTRACT.md), like the forward op.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+import _hiplib
+import nf4_grouped
+from nf4_grouped import (BLOCKSIZE, DECODE_MAX_ROWS, _aligned_rows, _bf16_activations,
+                         _check_host_ids, _eids_device, _require_gpu, _scales_view,
+                         _stream_ptr, to_device_i32)
+
+_SYNC_LOCK = threading.Lock()
+_SYNC = {}   # (device index, stream handle) -> int32 sync words, zero between calls
+
+
+def _sync_words(dev, G: int):
+    """The fused kernel's sync words for this device and stream. They start
+    at zero and every call leaves them at zero, so one buffer serves every
+    stream-ordered call; a separate buffer per stream keeps concurrent
+    streams apart."""
+    key = (dev.index, _stream_ptr(dev))
+    need = 2 + 2 * G
+    with _SYNC_LOCK:
+        buf = _SYNC.get(key)
+        if buf is None or buf.numel() < need:
+            buf = torch.zeros(max(need, 4096), dtype=torch.int32, device=dev)
+            _SYNC[key] = buf
+    return buf
+
+
+def ffn_sync_error(device=None) -> bool:
+    """True if a down unit of any fused call on this device gave up waiting
+    for its h (the output of that call is invalid). Reads device memory: it
+    synchronises, so it is meant for tests and diagnostics."""
+    dev = torch.device(device if device is not None else "cuda")
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    with _SYNC_LOCK:
+        bufs = [b for (d, _s), b in _SYNC.items() if d == idx]
+    return any(int(b[1].item()) != 0 for b in bufs)
+
+
+def silu_mul_locked(gu: torch.Tensor) -> torch.Tensor:
+    """``h = bf16(silu_locked(gu[:, :H]) * gu[:, H:])`` for bf16 ``gu [T, 2H]``
+    (one HIP launch). The activation of the fused FFN, unfused."""
+    _require_gpu(gu, "silu_mul_locked",
+                 "The CPU form is silu_locked_ref in the reference's cpu_grouped.")
+    if gu.dtype != torch.bfloat16:
+        raise TypeError(f"silu_mul_locked: gu must be bfloat16, got {gu.dtype}")
+    T, n2 = gu.shape
+    if n2 % 2 or (n2 // 2) % 8:
+        raise ValueError(f"gu width {n2} must be 2H with H % 8 == 0")
+    H = n2 // 2
+    if gu.stride(-1) != 1 or gu.stride(0) % 8 or gu.data_ptr() % 16:
+        gu = gu.contiguous()
+    h = torch.empty(T, H, dtype=torch.bfloat16, device=gu.device)
+    with torch.cuda.device(gu.device):
+        rc = _hiplib.load().gnf4_hip_silu_mul(gu.data_ptr(), gu.stride(0), T, H, h.data_ptr(),
+                                              h.stride(0), _stream_ptr(gu.device))
+    _hiplib.check(rc, "silu_mul_locked")
+    return h
+
+
+def _check(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids):
+    """The reference wrapper's checks (kernel/cpu_grouped.py:306-331)."""
+    T, K = a_cat.shape
+    assert sum(int(m) for m in sizes) == T, (sum(int(m) for m in sizes), T)
+    if gu_packed.dtype != torch.uint8 or dn_packed.dtype != torch.uint8:
+        raise TypeError("packed weights must be uint8")
+    if gu_absmax.dtype != torch.float32 or dn_absmax.dtype != torch.float32:
+        raise TypeError("absmax must be fp32")
+    n_gu = gu_packed.shape[1]
+    if n_gu % 2:
+        raise ValueError(f"gu output width {n_gu} must be even (gate/up halves)")
+    h_dim = n_gu // 2
+    if K % BLOCKSIZE or gu_packed.shape[2] * 2 != K:
+        raise ValueError("K mismatch or K % 64 != 0")
+    if h_dim % BLOCKSIZE or dn_packed.shape[2] * 2 != h_dim:
+        raise ValueError(f"dn expects K={h_dim} (=H) with H % 64 == 0, "
+                         f"got packed K={dn_packed.shape[2] * 2}")
+    if dn_packed.shape[0] != gu_packed.shape[0]:
+        raise ValueError("gu/dn expert counts differ")
+    E, n_dn = gu_packed.shape[0], dn_packed.shape[1]
+    if tuple(gu_absmax.shape) != (E, n_gu, K // BLOCKSIZE):
+        raise ValueError(f"gu_absmax shape {tuple(gu_absmax.shape)} != {(E, n_gu, K // 64)}")
+    if tuple(dn_absmax.shape) != (E, n_dn, h_dim // BLOCKSIZE):
+        raise ValueError(f"dn_absmax shape {tuple(dn_absmax.shape)} != "
+                         f"{(E, n_dn, h_dim // 64)}")
+    if len(sizes) != len(expert_ids):
+        raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
+    dev = a_cat.device
+    if any(t.device != dev for t in (gu_packed, gu_absmax, dn_packed, dn_absmax)):
+        raise ValueError("activations and weights must be on the same device")
+    return T, K, h_dim, n_dn
+
+
+def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes,
+                         expert_ids, fused: bool | None = None):
+    """Grouped NF4 expert FFN ``dn(silu(gate) * up)`` on the GPU.
+
+    ``a_cat [T, K]`` bf16 (fp16 / fp32 are rounded to bf16 first), rows sorted
+    by group; ``sizes`` per-group row counts (zero-size groups allowed);
+    ``expert_ids [G]`` list, CPU tensor or device tensor. Returns ``[T, N_dn]``
+    bf16. ``fused``: None picks the single fused launch when every group has at
+    most 16 rows; False forces the three-launch composition; True requires
+    the fused launch."""
+    _require_gpu(a_cat, "gemm_nf4_ffn_grouped",
+                 "The CPU form is the reference's gemm_nf4_ffn_grouped_cpu; a "
+                 "checkable decode of the weights is dequant_ref(packed, absmax, N, K).")
+    T, K, H, n_dn = _check(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes,
+                           expert_ids)
+    dev = a_cat.device
+    E = gu_packed.shape[0]
+    sizes_i = [int(m) for m in sizes]
+    G = len(sizes_i)
+    max_m = max(sizes_i, default=0)
+    if fused is None:
+        fused = max_m <= DECODE_MAX_ROWS
+    elif fused and max_m > DECODE_MAX_ROWS:
+        raise ValueError(f"the fused FFN launch takes groups of at most {DECODE_MAX_ROWS} "
+                         f"rows, got {max_m}")
+    if T == 0 or G == 0:
+        return torch.zeros(T, n_dn, dtype=torch.bfloat16, device=dev)
+    eids_dev = _eids_device(expert_ids, dev)
+    if eids_dev is None:
+        _check_host_ids(expert_ids, E)
+    if not fused:
+        gu = nf4_grouped.gemm_4bit_grouped(a_cat, gu_packed, gu_absmax, sizes, expert_ids)
+        h = silu_mul_locked(gu)
+        return nf4_grouped.gemm_4bit_grouped(h, dn_packed, dn_absmax, sizes, expert_ids)
+    a = _bf16_activations(a_cat, "gemm_nf4_ffn_grouped")
+    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
+    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
+    row_off = [0]
+    for m in sizes_i:
+        row_off.append(row_off[-1] + m)
+    host_eids = [] if eids_dev is not None else expert_ids
+    e_h, r_h = to_device_i32((host_eids, row_off), dev)
+    eids = eids_dev if eids_dev is not None else e_h
+    h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
+    sync = _sync_words(dev, G)
+    with torch.cuda.device(dev):
+        rc = _hiplib.load().gnf4_hip_nf4_ffn_fwd(
+            a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
+            Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
+            Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
+            eids.data_ptr(), r_h.data_ptr(), G, max(max_m, 1), 2 * H, K, n_dn,
+            h.data_ptr(), h.stride(0), sync.data_ptr(), sync.numel(),
+            out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    del e_h, r_h   # the index tensors stay alive until the launch is enqueued
+    _hiplib.check(rc, "gemm_nf4_ffn_grouped")
+    return out

@@ -404,6 +404,15 @@ def _eids_device(expert_ids, dev):
     return None
 
 
+def _check_host_ids(expert_ids, E: int) -> None:
+    """Host-side expert ids must index the stack: an out-of-range id would
+    make the kernel read outside the weights. Device-resident ids are the
+    caller's responsibility (checking them would synchronise)."""
+    ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else list(expert_ids)
+    if ids and (min(int(e) for e in ids) < 0 or max(int(e) for e in ids) >= E):
+        raise ValueError(f"expert id out of range [0, {E})")
+
+
 def _stream_ptr(dev) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -421,6 +430,8 @@ class GroupPlan:
         self.one_row_each = bool(sizes_i) and min(sizes_i) == 1 and self.max_m == 1
         dev = torch.device(device)
         ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else list(expert_ids)
+        self.max_id = max((int(e) for e in ids), default=-1)
+        self.min_id = min((int(e) for e in ids), default=0)
         self.decode = self.max_m <= DECODE_MAX_ROWS and block_m is None
         if self.decode:
             row_off = [0]
@@ -454,6 +465,8 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
     E, N, half = W.shape
     T, K = a_cat.shape
     dev = a_cat.device
+    if plan.min_id < 0 or plan.max_id >= E:
+        raise ValueError(f"expert id out of range [0, {E})")
     a_cat, W, S = (_bf16_activations(a_cat, "launch_planned"), _aligned_rows(W, 16),
                    _scales_view(S))
     if out is None:
@@ -483,6 +496,8 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     sizes_i = [int(m) for m in sizes]
     max_m = max(sizes_i)
     eids_dev = _eids_device(expert_ids, dev)
+    if eids_dev is None:
+        _check_host_ids(expert_ids, E)
     host_eids = [] if eids_dev is not None else expert_ids
     if max_m <= DECODE_MAX_ROWS and block_m is None:
         if min(sizes_i) == 1 and max_m == 1:
@@ -538,6 +553,8 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     bm = _kernel_block_m(_prefill_block_m(max(sizes_i)))
     t0, tr, tg = _tiles_host(sizes_i, bm)
     eids_dev = _eids_device(expert_ids, dev)
+    if eids_dev is None:
+        _check_host_ids(expert_ids, E)
     e_h, t0_d, tr_d, tg_d = to_device_i32(([] if eids_dev is not None else expert_ids,
                                            t0, tr, tg), dev)
     eids = eids_dev if eids_dev is not None else e_h

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 2
+#define GNF4_HIP_ABI_VERSION 3
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -103,6 +103,44 @@ int gnf4_hip_mxfp4_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *b
                        const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
                        int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
                        void *stream);
+
+/* Elementwise gate activation of the expert FFN, unfused form:
+ *   h[t, j] = bf16(silu_locked(gu[t, j]) * gu[t, H + j]),  j < H,
+ * gu [T, ldg] bf16 (gate = first H columns, up = next H), h [T, ldh] bf16.
+ * silu_locked is the reference's fixed fp32 op sequence
+ * (gnf4_native/cpu_kernels.c:776-822, kernel/cpu_grouped.py:147-179):
+ * clamp at +-87 with exact tails, degree-6 Horner 2^f, 1 / (1 + e), no FMA.
+ * H, ldg, ldh multiples of 8; gu and h 16-byte aligned. */
+int gnf4_hip_silu_mul(const void *gu, int64_t ldg, int64_t T, int64_t H, void *h,
+                      int64_t ldh, void *stream);
+
+/* Fused NF4 expert FFN at decode, one launch: out = dn(silu(gate) * up) with
+ * gate/up the two halves of a . W_gu^T. GPU counterpart of the reference's
+ * CPU gnf4_gemv_nf4_ffn_grouped (gnf4_native/cpu_kernels.c:948-986, spec
+ * kernel/cpu_grouped.py:182-194), which has no GPU kernel there.
+ *   a     [T, lda] bf16, rows sorted by group; every group <= 16 rows
+ *         (max_m = the largest, 1..16; row_off [G + 1] as for the decode
+ *         forward, NULL only when every group is one row).
+ *   W_gu  [E, N_gu, K/2] u8 + absmax [E, N_gu, K/64] f32, H = N_gu / 2,
+ *         H % 64 == 0, K % 64 == 0.
+ *   W_dn  [E, N_dn, H/2] u8 + absmax [E, N_dn, H/64] f32.
+ *   h     [T, ldh] bf16 workspace (the intermediate; ldh >= H, % 8 == 0).
+ *   sync  >= 2 + 2 G u32 words, zero before the first call; every call
+ *         leaves them zero again. Calls that overlap on one sync buffer race.
+ *         Word 1 becomes nonzero if a down unit gave up waiting for h (never
+ *         expected; the output is then invalid).
+ *   out   [T, ldo] bf16.
+ * h is bf16(silu_locked(bf16(gate)) * bf16(up)), so the result equals
+ * gnf4_hip_nf4_fwd (gate_up) -> gnf4_hip_silu_mul -> gnf4_hip_nf4_fwd (down)
+ * bit for bit. */
+int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *B_gu,
+                         int64_t gu_sbe, int64_t gu_sbn, const float *absmax_gu,
+                         int64_t gu_sae, int64_t gu_san, const uint8_t *B_dn,
+                         int64_t dn_sbe, int64_t dn_sbn, const float *absmax_dn,
+                         int64_t dn_sae, int64_t dn_san, const int32_t *expert_ids,
+                         const int32_t *row_off, int G, int max_m, int64_t N_gu, int64_t K,
+                         int64_t N_dn, void *h, int64_t ldh, uint32_t *sync,
+                         int64_t sync_words, void *out, int64_t ldo, void *stream);
 
 /* Grouped dgrad for either format: out[t, :] = grad_out[t, :] . dequant(W[e(t)]),
  * contracting over N in fixed 64-wide ascending steps (output bits do not

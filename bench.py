@@ -15,8 +15,10 @@ Also reported:
                with HIP events on its stream, against the 8 TB/s HBM peak.
   cpu_baseline the reference's own CPU kernels (gnf4_native/cpu_kernels.c
                compiled by oracle/Makefile) on the host cores, same shapes.
-  extra        batch 4 / 16 decode, GPT-OSS-20B MXFP4 decode, Qwen3 NF4
-               Zipf prefill and down-projection dgrad TFLOP/s.
+  extra        batch 4 / 16 decode, the fused expert FFN (gate_up -> silu *
+               up -> down in one launch) against its two- and three-launch
+               forms, GPT-OSS-20B MXFP4 decode, Qwen3 NF4 Zipf prefill and
+               down-projection dgrad TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -173,6 +175,61 @@ class DecodeModel:
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / (replays * self.L)
+
+
+    def ffn_ms(self, kind, replays=20):
+        """Average time (ms) of one layer's expert FFN, every layer captured
+        back to back in one graph and timed with HIP events on the launch
+        stream. kind: "pair" = gate_up and down launches only (no
+        activation), "composed" = gate_up -> silu-multiply -> down (three
+        launches), "fused" = the single fused launch."""
+        import torch
+        import nf4_ffn
+        from nf4_grouped import launch_planned
+        plans = self.plans()
+        outs = []
+        for l in range(self.L):
+            x = self.routes[l][2]
+            outs.append((torch.empty(x.shape[0], self.cfg["gu"][0], dtype=torch.bfloat16,
+                                     device=self.dev),
+                         torch.empty(x.shape[0], self.cfg["gu"][0] // 2, dtype=torch.bfloat16,
+                                     device=self.dev),
+                         torch.empty(x.shape[0], self.cfg["dn"][0], dtype=torch.bfloat16,
+                                     device=self.dev)))
+
+        def run():
+            for l in range(self.L):
+                sizes, eids, x, hin = self.routes[l]
+                gu, h, out = outs[l]
+                if kind == "fused":
+                    nf4_ffn.launch_ffn_planned(x, *self.gu[l], *self.dn[l], plans[l], h=h, out=out)
+                    continue
+                launch_planned(0, x, *self.gu[l], plans[l], out=gu)
+                if kind == "composed":
+                    h = nf4_ffn.silu_mul_locked(gu)
+                launch_planned(0, h if kind == "composed" else hin, *self.dn[l], plans[l], out=out)
+
+        _, graph = time_graph(run, 1, 2, self.dev)
+        stream = torch.cuda.current_stream(self.dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (replays * self.L)
+
+
+def ffn_report(model):
+    """Per-layer expert FFN at decode: the fused launch against the two- and
+    three-launch forms, and the fused form's packed-weight rate."""
+    per_layer = model.packed_bytes / model.L
+    r = {}
+    for kind in ("pair", "composed", "fused"):
+        ms = model.ffn_ms(kind)
+        r[f"{kind}_us_per_layer"] = round(ms * 1e3, 3)
+        r[f"{kind}_gbs"] = round(per_layer / (ms * 1e-3) / 1e9, 1)
+    return r
 
 
 def time_graph(fn, steps, warmup, dev):
@@ -383,6 +440,8 @@ def main():
         f"down {dn_ms * 1e3:.2f} us -> {dn_gbs:.1f} GB/s")
 
     extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1)}}
+    extra[f"qwen3_nf4_ffn_b{args.batch}"] = ffn_report(model)
+    log(f"[bench] ffn: {json.dumps(extra[f'qwen3_nf4_ffn_b{args.batch}'])}")
     if not args.no_extra:
         for b in (4, 16):
             m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=8)
@@ -390,6 +449,7 @@ def main():
             a2 = sum(m.bytes_dn) / len(m.bytes_dn) / (m.kernel_ms("dn") * 1e-3) / 1e9
             extra[f"qwen3_nf4_decode_b{b}"] = {"gate_up_gbs": round(a, 1), "down_gbs": round(a2, 1),
                                                "experts_per_layer": round(sum(len(r[0]) for r in m.routes) / m.L, 1)}
+            extra[f"qwen3_nf4_ffn_b{b}"] = ffn_report(m)
             del m
         for b in (1, 64):
             m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=6)

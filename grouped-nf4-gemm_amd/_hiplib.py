@@ -30,6 +30,7 @@ SIGNATURES = {
     "gnf4_hip_device_cus": [],
     "gnf4_hip_activations_to_bf16": [_P, _I, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
+    "gnf4_hip_ffn_sync_words": [_I, _I64, _I64],
     "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
                              _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
@@ -46,6 +47,9 @@ SIGNATURES = {
     "gnf4_hip_mxfp4_dgrad": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
 }
+
+# entry points that do not return int
+RESTYPES = {"gnf4_hip_ffn_sync_words": ctypes.c_int64}
 
 _lib = None
 
@@ -68,7 +72,7 @@ def load():
     for name, args in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = args
-        fn.restype = ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     ver = lib.gnf4_hip_abi_version()
     if ver != ABI_VERSION:
         raise HipLibraryError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}: rebuild it")

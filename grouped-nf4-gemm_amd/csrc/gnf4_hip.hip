@@ -229,6 +229,16 @@ __device__ __forceinline__ u32x4_t buf_load16(__amdgpu_buffer_rsrc_t r, int off)
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Cache-policy bits of a buffer access: kScopeDevice (sc1) makes the access
+// coherent at device scope, across the XCDs' separate L2 caches, without any
+// cache writeback or invalidate.
+constexpr int kScopeDevice = 16;
+
+template <int kAux>
+__device__ __forceinline__ u32x4_t buf_load16_aux(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAux));
+}
+
 __device__ __forceinline__ unsigned buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
@@ -265,6 +275,7 @@ __device__ __forceinline__ float load_scale(const FwdArgs& p, int64_t e, int64_t
 //   kFfnDn   fused FFN, second stage: a plain unit over h whose weight
 //            loads are issued before it waits for h to be complete.
 constexpr int kPlain = 0, kFfnGu = 1, kFfnDn = 2;
+constexpr int kFfnFlagBase = 16;   // first flag word of the fused FFN's sync buffer
 
 struct NoWait {
   __device__ void operator()() const {}
@@ -321,7 +332,11 @@ template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPiece
           class Wait>
 __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, char* smem,
                                             const int lut, const int64_t ffn_h,
+                                            const int64_t ffn_n_dn, uint32_t* ffn_sync,
                                             const Wait& wait_acts) {
+  // kFfnDn reads h, written by other workgroups during this launch, with
+  // device-scope loads
+  constexpr int kActAux = kKind == kFfnDn ? kScopeDevice : 0;
   static_assert(kKind != kFfnGu || (FMT == kNF4 && kTiles == 2), "gate/up pairs need 2 tiles");
   float2* s_tab = reinterpret_cast<float2*>(smem);
   constexpr int kThreadsD = 64 * kDecodeWaves;
@@ -356,7 +371,8 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, c
       const int pc = (int)threadIdx.x + i * kThreadsD;
       if (wave * 64 + i * kThreadsD < pieces) {         // uniform: whole waves skip
         const int m = pc / kslices, sl = pc - m * kslices;
-        av[i] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+        av[i] = buf_load16_aux<kActAux>(
+            ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
       }
     }
   };
@@ -407,7 +423,7 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, c
         // rows >= M fall outside the activation resource and load as zeros
         const int aoff = oob_unless(kval, (int)((int64_t)nl * p.lda * 2) + (int)kseg * 2);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16(ra, aoff + 16 * j);
+        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16_aux<kActAux>(ra, aoff + 16 * j);
       }
     };
 #pragma unroll
@@ -507,15 +523,28 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, c
         vg = vg + s_red[(w * kTiles) * 64 + lane];
         vu = vu + s_red[(w * kTiles + 1) * 64 + lane];
       }
-      const int64_t col = nu * 16 + nl;
+      // h goes out with device-scope stores; once the wave's stores have
+      // completed (vmcnt 0) they are visible to device-scope loads on every
+      // XCD, and lane 0 counts the unit for its group
+      const __amdgpu_buffer_rsrc_t rh =
+          make_rsrc(p.out + (int64_t)r0 * p.ldo, (int64_t)M * p.ldo * 2);
+      const int col = (int)(nu * 16 + nl);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 4 * q + i;
-        if (m < M) {
-          const float hv = silu_locked(bf16_round(vg[i])) * bf16_round(vu[i]);
-          p.out[(int64_t)(r0 + m) * p.ldo + col] = f32_to_bf16_bits(hv);
-        }
+        const float hv = silu_locked(bf16_round(vg[i])) * bf16_round(vu[i]);
+        const int off = oob_unless(m < M, (int)(((int64_t)m * p.ldo + col) * 2));
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(hv), rh, off, 0, kScopeDevice);
       }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      // one flag in the private row of every down unit of the group:
+      // flags[(g * dn_per_group + d) * gu_per_group + nu]
+      const int64_t gu_per_group = ffn_h / 16;
+      const int64_t dn_per_group = (ffn_n_dn + 31) / 32;
+      uint32_t* row0 = ffn_sync + kFfnFlagBase + (int64_t)g * dn_per_group * gu_per_group + nu;
+      for (int64_t d = lane; d < dn_per_group; d += 64)
+        __hip_atomic_store(row0 + d * gu_per_group, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
   } else {
     // wave t < kTiles sums tile t over the waves in wave order (deterministic)
@@ -544,88 +573,84 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
   __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
   decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain>(
-      p, (int64_t)blockIdx.x, smem, lut, 0, NoWait{});
+      p, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, NoWait{});
 }
 
 // ------------------------------------------------------------ fused FFN --
 //
 // gate_up -> silu(gate) * up -> down for groups of at most 16 rows, in one
-// launch. Units are numbered by a ticket taken when a workgroup starts, so
-// numbers are handed out in start order: the G * (H / 16) gate/up units come
-// first, then the G * ceil(N_dn / 32) down units. A gate/up unit writes its
-// 16 columns of h (bf16, [T, ldh]) and then bumps its group's counter with
-// release semantics; a down unit issues its weight loads, waits until its
-// group's counter shows every gate/up unit of the group (acquire), and then
-// reads h. A down unit only ever waits on units with smaller tickets, which
-// are running or done, so the wait always ends.
+// launch. Workgroups [0, G * H / 16) are gate/up units, the rest are down
+// units (G * ceil(N_dn / 32)), both in group-major order. A down unit only
+// waits on gate/up units, which have smaller ids; workgroups are dispatched
+// in id order and gate/up units never wait, so the wait always ends. (A bounded spin backs this up: a unit that polls
+// kFfnSpinLimit times sets the error word and goes on.)
 //
-// Sync words (u32, device memory, zero before the first call): [0] ticket,
-// [1] error flag, [2 + 2g] group g's arrivals, [3 + 2g] its departures.
-// Every word is back at zero when a call ends: the workgroup that takes the
-// last ticket subtracts the call's ticket count, and the last down unit of a
-// group to pass its wait clears that group's pair. Stream-ordered calls can
-// therefore share one sync buffer; calls that overlap on it race.
+// Hand-off without cache maintenance or atomics: a gate/up unit writes its
+// 16 columns of h (bf16, [T, ldh]) with device-scope stores, waits for them
+// to complete, and then sets its flag in the private flag row of every down
+// unit of its group (device-scope stores). A down unit issues its weight
+// loads, polls its own row with one device-scope vector load until every
+// flag is set, reads h with device-scope loads, and clears its row: it is
+// the row's only reader, so the words are zero again for the next call (and
+// for graph replays) without any counting. Release/acquire fences would
+// write back or invalidate whole L2 caches per unit, and same-address
+// atomics serialise at about 0.1 us each; both cost more than the launch
+// this saves.
+//
+// Sync words (u32, device memory, zero before the first call): [0] error
+// flag, then G * ceil(N_dn / 32) rows of H / 16 flags from word
+// kFfnFlagBase. Calls that overlap on one sync buffer race.
 constexpr int kFfnSpinLimit = 1 << 22;   // polls before a down unit gives up
-constexpr int kFfnMaxDynLds = 159 * 1024; // dynamic LDS beside the static ticket word
+constexpr int kFfnMaxDynLds = 160 * 1024;
 
 template <int CPW1, int CPW2, int kAPieces>
 __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const FwdArgs dn,
-                                                       const int64_t H, uint32_t* sync,
-                                                       const uint32_t n_tickets) {
+                                                       const int64_t H, uint32_t* sync) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  __shared__ uint32_t s_ticket;
-  if (threadIdx.x == 0) {
-    const uint32_t t =
-        __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (t == n_tickets - 1)   // every ticket of this call is taken
-      __hip_atomic_fetch_add(sync, 0u - n_tickets, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_ticket = t;
-  }
-  __syncthreads();
-  const int64_t u = (int64_t)s_ticket;
   const int lut = nf4_lut_lane();
   __builtin_amdgcn_sched_barrier(0);
+  // every gate/up unit (group-major) comes before every down unit: the
+  // gate/up phase runs at full width, and a down unit that starts early
+  // streams its weights while the last gate/up units finish
   const int64_t gu_per_group = H / 16;
+  const int64_t dn_per_group = (dn.N + 31) / 32;
   const int64_t gu_units = (int64_t)gu.G * gu_per_group;
+  const int64_t u = blockIdx.x;
   if (u < gu_units) {
-    const int g = (int)(u / gu_per_group);
-    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, u, smem, lut, H, NoWait{});
-    const int M = gu.row_off ? gu.row_off[g + 1] - gu.row_off[g] : 1;
-    if (M <= 0) return;                 // empty group: nobody waits on it
-    // every thread's h stores are complete and visible at agent scope
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(sync + 2 + 2 * g, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, u, smem, lut, H, dn.N, sync,
+                                                     NoWait{});
     return;
   }
-  const int64_t dn_per_group = (dn.N + 31) / 32;
-  const int64_t u2 = u - gu_units;
-  const int g = (int)(u2 / dn_per_group);
+  const int64_t d = u - gu_units;
+  const int g = (int)(d / dn_per_group);
+  const int M = dn.row_off ? dn.row_off[g + 1] - dn.row_off[g] : 1;
+  if (M <= 0) return;                   // empty group: no gate/up unit sets its flags
+  uint32_t* row = sync + kFfnFlagBase + d * gu_per_group;
   auto wait_h = [&]() {
-    if (threadIdx.x == 0) {
-      uint32_t* arrived = sync + 2 + 2 * g;
+    if (threadIdx.x < 64) {             // wave 0 polls the row, 64 flags per load
+      const int lane = threadIdx.x;
       int spins = 0;
-      while (__hip_atomic_load(arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             (uint32_t)gu_per_group) {
+      while (true) {
+        bool all = true;
+        for (int64_t j = lane; j < gu_per_group; j += 64)
+          all &= __hip_atomic_load(row + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+        if (__builtin_amdgcn_ballot_w64(!all) == 0) break;
         if (++spins > kFfnSpinLimit) {   // not expected: flag it and go on
-          __hip_atomic_store(sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (lane == 0)
+            __hip_atomic_store(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
         }
-        __builtin_amdgcn_s_sleep(2);
+        __builtin_amdgcn_s_sleep(1);
       }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      // the group's last unit past this point clears its pair for the next call
-      if (__hip_atomic_fetch_add(sync + 3 + 2 * g, 1u, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)dn_per_group - 1) {
-        __hip_atomic_store(arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(sync + 3 + 2 * g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      for (int64_t j = lane; j < gu_per_group; j += 64)   // this row's only reader
+        __hip_atomic_store(row + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // no wave issues an h load before wave 0 has seen every flag (the weight
+    // loads already in flight need not land first)
     __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    asm volatile("" ::: "memory");
   };
-  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, u2, smem, lut, 0, wait_h);
+  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, d, smem, lut, 0, 0, sync, wait_h);
 }
 
 // Elementwise silu-multiply for the unfused path (and groups too large for
@@ -1741,7 +1766,7 @@ int launch_decode(const FwdArgs& p, hipStream_t stream) {
 // gate/up over K, down over H; the chunk split per wave follows each K.
 template <int CPW1, int CPW2, int PA>
 int launch_ffn_inst(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
-                    uint32_t n_tickets, int lds, hipStream_t stream) {
+                    uint32_t n_units, int lds, hipStream_t stream) {
   static int configured_dev = -1;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -2;
@@ -1752,28 +1777,28 @@ int launch_ffn_inst(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* s
       return -2;
     configured_dev = dev;
   }
-  hipLaunchKernelGGL((k_ffn_decode<CPW1, CPW2, PA>), dim3(n_tickets), dim3(512), lds, stream,
-                     gu, dn, H, sync, n_tickets);
+  hipLaunchKernelGGL((k_ffn_decode<CPW1, CPW2, PA>), dim3(n_units), dim3(512), lds, stream,
+                     gu, dn, H, sync);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 template <int CPW1, int CPW2>
 int launch_ffn_pa(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
-                  uint32_t n_tickets, int pa, int lds, hipStream_t stream) {
+                  uint32_t n_units, int pa, int lds, hipStream_t stream) {
   switch (pa) {
-    case 1: return launch_ffn_inst<CPW1, CPW2, 1>(gu, dn, H, sync, n_tickets, lds, stream);
-    case 2: return launch_ffn_inst<CPW1, CPW2, 2>(gu, dn, H, sync, n_tickets, lds, stream);
-    case 4: return launch_ffn_inst<CPW1, CPW2, 4>(gu, dn, H, sync, n_tickets, lds, stream);
-    default: return launch_ffn_inst<CPW1, CPW2, 0>(gu, dn, H, sync, n_tickets, lds, stream);
+    case 1: return launch_ffn_inst<CPW1, CPW2, 1>(gu, dn, H, sync, n_units, lds, stream);
+    case 2: return launch_ffn_inst<CPW1, CPW2, 2>(gu, dn, H, sync, n_units, lds, stream);
+    case 4: return launch_ffn_inst<CPW1, CPW2, 4>(gu, dn, H, sync, n_units, lds, stream);
+    default: return launch_ffn_inst<CPW1, CPW2, 0>(gu, dn, H, sync, n_units, lds, stream);
   }
 }
 
 int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
                hipStream_t stream) {
   constexpr int kW = 8;
-  const int64_t tickets = (int64_t)gu.G * (H / 16) + (int64_t)gu.G * ((dn.N + 31) / 32);
-  if (tickets <= 0) return 0;
-  if (tickets > 0x7FFFFFFF) return -1;
+  const int64_t units = (int64_t)gu.G * (H / 16) + (int64_t)gu.G * ((dn.N + 31) / 32);
+  if (units <= 0) return 0;
+  if (units > 0x7FFFFFFF) return -1;
   const int64_t kmax = gu.K > dn.K ? gu.K : dn.K;
   const bool stage = gu.max_m <= 2 && (int64_t)gu.max_m * kmax * 2 <= 4 * 64 * kW * 16;
   const int64_t a_bytes = stage ? (int64_t)gu.max_m * kmax * 2 : 0;
@@ -1785,7 +1810,7 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
   if (lds > kFfnMaxDynLds) return -1;
   const bool two1 = ((gu.K + 127) / 128 + kW - 1) / kW > 1;
   const bool two2 = ((dn.K + 127) / 128 + kW - 1) / kW > 1;
-  const uint32_t n = (uint32_t)tickets;
+  const uint32_t n = (uint32_t)units;
   if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
   if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, sync, n, pa, (int)lds, stream);
   if (two2) return launch_ffn_pa<1, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
@@ -1985,6 +2010,11 @@ int gnf4_hip_silu_mul(const void* gu, int64_t ldg, int64_t T, int64_t H, void* h
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+int64_t gnf4_hip_ffn_sync_words(int G, int64_t N_gu, int64_t N_dn) {
+  if (G < 0 || N_gu <= 0 || N_dn <= 0) return -1;
+  return kFfnFlagBase + (int64_t)G * ((N_dn + 31) / 32) * (N_gu / 32);
+}
+
 int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* B_gu,
                          int64_t gu_sbe, int64_t gu_sbn, const float* absmax_gu,
                          int64_t gu_sae, int64_t gu_san, const uint8_t* B_dn, int64_t dn_sbe,
@@ -2005,7 +2035,8 @@ int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t*
   if (gu_sbn % 16 || gu_sbe % 16 || dn_sbn % 16 || dn_sbe % 16 || !aligned16(B_gu) ||
       !aligned16(B_dn))
     return -1;
-  if (sync_words < 2 + 2 * (int64_t)G || ((reinterpret_cast<uintptr_t>(sync) & 3) != 0))
+  if (sync_words < gnf4_hip_ffn_sync_words(G, N_gu, N_dn) ||
+      ((reinterpret_cast<uintptr_t>(sync) & 3) != 0))
     return -1;
   if (G == 0) return 0;
   FwdArgs gu{};

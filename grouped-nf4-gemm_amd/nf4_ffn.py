@@ -36,17 +36,30 @@ from nf4_grouped import (BLOCKSIZE, DECODE_MAX_ROWS, _aligned_rows, _bf16_activa
                          _check_host_ids, _eids_device, _require_gpu, _scales_view,
                          _stream_ptr, to_device_i32)
 
+# Auto path choice: the fused launch saves the silu launch and a kernel
+# boundary, and pays a device-scope hand-off per unit (h stores must complete
+# before the flags go out, and down units hold their slot while they wait).
+# Measured on MI355X at Qwen3-30B-A3B shapes (per layer, HIP graph): batch 1
+# 14.4 us fused vs 16.5 us three-launch, batch 4 37.4 vs 39.0, batch 8 63.0
+# vs 60.7 -- the fused launch wins up to about 4000 workgroup units.
+FUSED_MAX_UNITS = 4096
+
+
+def _fused_units(G: int, H: int, n_dn: int) -> int:
+    return G * (H // 16 + (n_dn + 31) // 32)
+
+
 _SYNC_LOCK = threading.Lock()
 _SYNC = {}   # (device index, stream handle) -> int32 sync words, zero between calls
 
 
-def _sync_words(dev, G: int):
+def _sync_words(dev, G: int, n_gu: int, n_dn: int):
     """The fused kernel's sync words for this device and stream. They start
     at zero and every call leaves them at zero, so one buffer serves every
     stream-ordered call; a separate buffer per stream keeps concurrent
     streams apart."""
     key = (dev.index, _stream_ptr(dev))
-    need = 2 + 2 * G
+    need = int(_hiplib.load().gnf4_hip_ffn_sync_words(G, n_gu, n_dn))
     with _SYNC_LOCK:
         buf = _SYNC.get(key)
         if buf is None or buf.numel() < need:
@@ -63,7 +76,7 @@ def ffn_sync_error(device=None) -> bool:
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     with _SYNC_LOCK:
         bufs = [b for (d, _s), b in _SYNC.items() if d == idx]
-    return any(int(b[1].item()) != 0 for b in bufs)
+    return any(int(b[0].item()) != 0 for b in bufs)
 
 
 def silu_mul_locked(gu: torch.Tensor) -> torch.Tensor:
@@ -89,8 +102,15 @@ def silu_mul_locked(gu: torch.Tensor) -> torch.Tensor:
 
 def _check(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids):
     """The reference wrapper's checks (kernel/cpu_grouped.py:306-331)."""
-    T, K = a_cat.shape
+    T = a_cat.shape[0]
     assert sum(int(m) for m in sizes) == T, (sum(int(m) for m in sizes), T)
+    if len(sizes) != len(expert_ids):
+        raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
+    return _check_shapes(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax)
+
+
+def _check_shapes(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax):
+    T, K = a_cat.shape
     if gu_packed.dtype != torch.uint8 or dn_packed.dtype != torch.uint8:
         raise TypeError("packed weights must be uint8")
     if gu_absmax.dtype != torch.float32 or dn_absmax.dtype != torch.float32:
@@ -112,8 +132,6 @@ def _check(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert_ids)
     if tuple(dn_absmax.shape) != (E, n_dn, h_dim // BLOCKSIZE):
         raise ValueError(f"dn_absmax shape {tuple(dn_absmax.shape)} != "
                          f"{(E, n_dn, h_dim // 64)}")
-    if len(sizes) != len(expert_ids):
-        raise ValueError(f"{len(sizes)} group sizes but {len(expert_ids)} expert ids")
     dev = a_cat.device
     if any(t.device != dev for t in (gu_packed, gu_absmax, dn_packed, dn_absmax)):
         raise ValueError("activations and weights must be on the same device")
@@ -128,8 +146,9 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     by group; ``sizes`` per-group row counts (zero-size groups allowed);
     ``expert_ids [G]`` list, CPU tensor or device tensor. Returns ``[T, N_dn]``
     bf16. ``fused``: None picks the single fused launch when every group has at
-    most 16 rows; False forces the three-launch composition; True requires
-    the fused launch."""
+    most 16 rows and the launch has at most ``FUSED_MAX_UNITS`` workgroup
+    units (where it measures faster); False forces the three-launch
+    composition; True requires the fused launch. Both give the same bits."""
     _require_gpu(a_cat, "gemm_nf4_ffn_grouped",
                  "The CPU form is the reference's gemm_nf4_ffn_grouped_cpu; a "
                  "checkable decode of the weights is dequant_ref(packed, absmax, N, K).")
@@ -141,7 +160,7 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     G = len(sizes_i)
     max_m = max(sizes_i, default=0)
     if fused is None:
-        fused = max_m <= DECODE_MAX_ROWS
+        fused = max_m <= DECODE_MAX_ROWS and _fused_units(G, H, n_dn) <= FUSED_MAX_UNITS
     elif fused and max_m > DECODE_MAX_ROWS:
         raise ValueError(f"the fused FFN launch takes groups of at most {DECODE_MAX_ROWS} "
                          f"rows, got {max_m}")
@@ -165,7 +184,7 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     eids = eids_dev if eids_dev is not None else e_h
     h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
     out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
-    sync = _sync_words(dev, G)
+    sync = _sync_words(dev, G, 2 * H, n_dn)
     with torch.cuda.device(dev):
         rc = _hiplib.load().gnf4_hip_nf4_ffn_fwd(
             a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
@@ -177,3 +196,37 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     del e_h, r_h   # the index tensors stay alive until the launch is enqueued
     _hiplib.check(rc, "gemm_nf4_ffn_grouped")
     return out
+
+
+def launch_ffn_planned(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, plan, h=None,
+                       out=None):
+    """Fused FFN launch with a prepared decode ``nf4_grouped.GroupPlan``: the
+    kernel and nothing else (no table upload), for graph capture and timing
+    loops. ``a_cat`` bf16; ``h`` / ``out`` optional preallocated workspace
+    and result."""
+    if not plan.decode:
+        raise ValueError("launch_ffn_planned needs a decode plan (every group <= 16 rows)")
+    T, K, H, n_dn = _check_shapes(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax)
+    E = gu_packed.shape[0]
+    if plan.min_id < 0 or plan.max_id >= E:
+        raise ValueError(f"expert id out of range [0, {E})")
+    dev = a_cat.device
+    a = _bf16_activations(a_cat, "launch_ffn_planned")
+    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
+    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
+    if h is None:
+        h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
+    sync = _sync_words(dev, plan.G, 2 * H, n_dn)
+    with torch.cuda.device(dev):
+        rc = _hiplib.load().gnf4_hip_nf4_ffn_fwd(
+            a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
+            Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
+            Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
+            plan.eids.data_ptr(), plan.row_off.data_ptr(), plan.G, max(plan.max_m, 1), 2 * H,
+            K, n_dn, h.data_ptr(), h.stride(0), sync.data_ptr(), sync.numel(),
+            out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    _hiplib.check(rc, "launch_ffn_planned")
+    return out
+

@@ -125,14 +125,21 @@ int gnf4_hip_silu_mul(const void *gu, int64_t ldg, int64_t T, int64_t H, void *h
  *         H % 64 == 0, K % 64 == 0.
  *   W_dn  [E, N_dn, H/2] u8 + absmax [E, N_dn, H/64] f32.
  *   h     [T, ldh] bf16 workspace (the intermediate; ldh >= H, % 8 == 0).
- *   sync  >= 2 + 2 G u32 words, zero before the first call; every call
- *         leaves them zero again. Calls that overlap on one sync buffer race.
- *         Word 1 becomes nonzero if a down unit gave up waiting for h (never
+ *   sync  >= gnf4_hip_ffn_sync_words(G, N_gu, N_dn) u32 words, zero
+ *         before the first call; every call leaves them zero again (graph
+ *         replays included). Calls that overlap on one sync buffer race.
+ *         Word 0 becomes nonzero if a down unit gave up waiting for h (never
  *         expected; the output is then invalid).
  *   out   [T, ldo] bf16.
  * h is bf16(silu_locked(bf16(gate)) * bf16(up)), so the result equals
  * gnf4_hip_nf4_fwd (gate_up) -> gnf4_hip_silu_mul -> gnf4_hip_nf4_fwd (down)
  * bit for bit. */
+/* Size (u32 words) of the sync buffer gnf4_hip_nf4_ffn_fwd needs for G
+ * groups: one flag per (gate/up unit, down unit) pair of a group, plus a
+ * header. -1 on bad arguments. No counterpart in the reference (its fused
+ * FFN is CPU-only). */
+int64_t gnf4_hip_ffn_sync_words(int G, int64_t N_gu, int64_t N_dn);
+
 int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *B_gu,
                          int64_t gu_sbe, int64_t gu_sbn, const float *absmax_gu,
                          int64_t gu_sae, int64_t gu_san, const uint8_t *B_dn,

@@ -15,7 +15,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "gnf4_hip.h"
 def declared_functions():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return re.findall(r"^\s*int\s+(gnf4_hip_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|int64_t)\s+(gnf4_hip_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_the_expected_entry_points():
@@ -76,3 +76,13 @@ def test_widening_rejects_bad_arguments_without_a_device():
     assert w(8, _hiplib.DTYPE_F32, 2, 64, 64, 16, 64, None) == -1     # 16-byte alignment
     assert w(None, _hiplib.DTYPE_F32, 2, 64, 64, 16, 64, None) == -1
     assert w(None, _hiplib.DTYPE_F16, 0, 64, 64, None, 64, None) == 0  # nothing to do
+
+
+def test_ffn_sync_size_is_the_flag_count_plus_header():
+    lib = _hiplib.load()
+    words = lib.gnf4_hip_ffn_sync_words
+    # Qwen3 shapes, batch 1: 8 groups x 64 down units x 48 gate/up units
+    assert words(8, 1536, 2048) == 16 + 8 * 64 * 48
+    assert words(0, 1536, 2048) == 16
+    assert words(3, 128, 24) == 16 + 3 * 1 * 4
+    assert words(-1, 128, 24) == -1

@@ -90,7 +90,7 @@ def test_fused_equals_the_three_launch_composition_qwen3_shape(sizes, ids):
     nf4_ffn, _ = _mods()
     gu_p, gu_a, dn_p, dn_a = _stack(QWEN["E"], QWEN["H"], QWEN["K"], QWEN["N_dn"], seed=3)
     a = rand_acts(sum(sizes), QWEN["K"], seed=4)
-    out = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
+    out = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
     ref = _composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
     assert out.shape == (sum(sizes), QWEN["N_dn"]) and out.dtype == torch.bfloat16
     assert torch.equal(_bits(out), _bits(ref))
@@ -104,7 +104,7 @@ def test_fused_equals_composition_other_shapes(H, K, N_dn):
     gu_p, gu_a, dn_p, dn_a = _stack(6, H, K, N_dn, seed=H + K)
     sizes, ids = [1, 4, 2, 1], [5, 0, 3, 1]
     a = rand_acts(sum(sizes), K, seed=5)
-    out = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
+    out = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
     assert torch.equal(_bits(out), _bits(_composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)))
 
 
@@ -236,3 +236,23 @@ def test_decode_staging_bound_large_k():
     out = gemm_4bit_grouped(a, W, S, sizes, ids)
     ref = torch.from_numpy(oracle_fwd("nf4", a, W, S, sizes, ids))
     assert rel_err(out.float().cpu(), ref) < 1e-2
+
+
+def test_many_groups_fused_and_auto_agree():
+    """B = 16 routing (about 80 groups, above the auto threshold): the fused
+    launch still gives the composition's bits, and the auto choice (the
+    composition here) agrees."""
+    nf4_ffn, _ = _mods()
+    gu_p, gu_a, dn_p, dn_a = _stack(QWEN["E"], QWEN["H"], QWEN["K"], QWEN["N_dn"], seed=50)
+    rng = np.random.default_rng(51)
+    counts = np.zeros(QWEN["E"], np.int64)
+    for _ in range(16):
+        counts[rng.choice(QWEN["E"], 8, replace=False)] += 1
+    ids = [int(e) for e in np.nonzero(counts)[0]]
+    sizes = [int(counts[e]) for e in ids]
+    assert nf4_ffn._fused_units(len(ids), QWEN["H"], QWEN["N_dn"]) > nf4_ffn.FUSED_MAX_UNITS
+    a = rand_acts(sum(sizes), QWEN["K"], seed=52)
+    fused = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
+    auto = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
+    assert torch.equal(_bits(fused), _bits(auto))
+    assert not nf4_ffn.ffn_sync_error()

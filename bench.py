@@ -17,7 +17,8 @@ Also reported:
                compiled by oracle/Makefile) on the host cores, same shapes.
   extra        batch 4 / 16 decode, the fused expert FFN (gate_up -> silu *
                up -> down in one launch) against its two- and three-launch
-               forms, GPT-OSS-20B MXFP4 decode, Qwen3 NF4 Zipf prefill and
+               forms, a whole device-routed decode MoE layer (top-k ->
+               grouping -> gather -> FFN -> combine, one graph), GPT-OSS-20B MXFP4 decode, Qwen3 NF4 Zipf prefill and
                down-projection dgrad TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
@@ -220,6 +221,35 @@ class DecodeModel:
         return e0.elapsed_time(e1) / (replays * self.L)
 
 
+def moe_layer_ms(model, replays=20):
+    """Average time (ms) of one whole decode MoE expert layer with device
+    routing: router logits -> top-k (renormalised softmax) + grouping +
+    gather (one launch) -> expert FFN -> weighted combine, every layer
+    captured back to back in one graph (nothing is read on the host)."""
+    import torch
+    import nf4_route
+    g = torch.Generator(device=model.dev).manual_seed(99)
+    logits = [torch.randn(model.batch, model.cfg["E"], generator=g, device=model.dev)
+              for _ in range(model.L)]
+    xs = [torch.randn(model.batch, model.cfg["gu"][1], generator=g, device=model.dev)
+          .to(torch.bfloat16) for _ in range(model.L)]
+
+    def run():
+        for l in range(model.L):
+            nf4_route.moe_layer(xs[l], logits[l], model.cfg["top_k"], *model.gu[l],
+                                *model.dn[l], mode=0, norm=True)
+
+    _, graph = time_graph(run, 1, 2, model.dev)
+    stream = torch.cuda.current_stream(model.dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (replays * model.L)
+
+
 def ffn_report(model):
     """Per-layer expert FFN at decode: the fused launch against the two- and
     three-launch forms, and the fused form's packed-weight rate."""
@@ -229,6 +259,8 @@ def ffn_report(model):
         ms = model.ffn_ms(kind)
         r[f"{kind}_us_per_layer"] = round(ms * 1e3, 3)
         r[f"{kind}_gbs"] = round(per_layer / (ms * 1e-3) / 1e9, 1)
+    if model.batch <= 16:
+        r["device_routed_layer_us"] = round(moe_layer_ms(model) * 1e3, 3)
     return r
 
 

@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -34,6 +34,12 @@ SIGNATURES = {
     "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
                              _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+    "gnf4_hip_route_topk": [_P, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64, _P],
+    "gnf4_hip_route_groups": [_P, _I64, _I64, _I, _I64, _I, _P, _P, _P, _P, _P, _P],
+    "gnf4_hip_route_decode": [_P, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64, _P, _I64,
+                              _I64, _I, _P, _P, _P, _P, _P, _P, _I64, _P],
+    "gnf4_hip_gather_rows": [_P, _I64, _P, _I64, _I, _I64, _P, _I64, _P],
+    "gnf4_hip_route_combine": [_P, _I64, _P, _P, _I64, _I64, _I, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_fwd": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_nf4_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,

@@ -1,7 +1,8 @@
 """Build libgnf4_hip.so in-tree for gfx950 with hipcc.
 
-``python build.py`` (or ``build()``) compiles csrc/gnf4_hip.hip into
-``libgnf4_hip.so`` next to this file. It always recompiles: the library must
+``python build.py`` (or ``build()``) compiles the HIP sources in csrc/ (the
+grouped GEMM kernels and the routing kernels) into ``libgnf4_hip.so`` next to
+this file. It always recompiles: the library must
 track its source, and the GPU box only ever loads the prebuilt file.
 """
 from __future__ import annotations
@@ -12,7 +13,7 @@ import subprocess
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
-SRC = HERE / "csrc" / "gnf4_hip.hip"
+SRCS = [HERE / "csrc" / "gnf4_hip.hip", HERE / "csrc" / "gnf4_route.hip"]
 OUT = HERE / "libgnf4_hip.so"
 ARCH = os.environ.get("GNF4_HIP_ARCH", "gfx950")
 
@@ -34,7 +35,7 @@ def hipcc() -> str:
 
 def build(verbose: bool = False) -> Path:
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), str(SRC)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), *(str(p) for p in SRCS)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so.
     noise = "is not a recognized feature for this target"

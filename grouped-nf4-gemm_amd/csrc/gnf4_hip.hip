@@ -656,13 +656,14 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
 // Elementwise silu-multiply for the unfused path (and groups too large for
 // the fused decode kernel): h[t, j] = bf16(silu_locked(gu[t, j]) * gu[t, H + j]),
 // gu bf16 [T, ldg], h bf16 [T, ldh]. Eight columns per thread.
+template <class Idx>
 __global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ gu, int64_t ldg,
-                                                  uint16_t* __restrict__ h, int64_t ldh,
-                                                  int64_t T, int64_t H) {
-  const int64_t vec = H / 8, total = T * vec;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / vec, c = (i - t * vec) * 8;
+                                                  uint16_t* __restrict__ h, int64_t ldh, Idx T,
+                                                  Idx H) {
+  const Idx vec = H / 8, total = T * vec;
+  for (Idx i = (Idx)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (Idx)gridDim.x * blockDim.x) {
+    const int64_t t = i / vec, c = (i - (Idx)t * vec) * 8;
     const u32x4_t gv = *reinterpret_cast<const u32x4_t*>(gu + t * ldg + c);
     const u32x4_t uv = *reinterpret_cast<const u32x4_t*>(gu + t * ldg + H + c);
     u32x4_t o;
@@ -1929,14 +1930,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
-template <class SrcT>
+// Idx is uint32_t whenever rows * cols / 8 < 2^32: 64-bit division is a long
+// software sequence on this GPU.
+template <class SrcT, class Idx>
 __global__ void __launch_bounds__(256) k_widen_to_bf16(const SrcT* __restrict__ src, int64_t ld_src,
                                                        uint16_t* __restrict__ dst, int64_t ld_dst,
-                                                       int64_t rows, int64_t vec_per_row) {
-  const int64_t total = rows * vec_per_row;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / vec_per_row, c = (i - r * vec_per_row) * 8;
+                                                       Idx rows, Idx vec_per_row) {
+  const Idx total = rows * vec_per_row;
+  for (Idx i = (Idx)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (Idx)gridDim.x * blockDim.x) {
+    const int64_t r = i / vec_per_row, c = (i - (Idx)r * vec_per_row) * 8;
     float v[8];
     if constexpr (sizeof(SrcT) == 2) {
       typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -1984,12 +1987,21 @@ int gnf4_hip_activations_to_bf16(const void* src, int src_dtype, int64_t rows, i
   const int64_t vec = cols / 8, work = (rows * vec + 255) / 256;
   const int64_t grid = clamp_grid(work, (int64_t)cus * 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (src_dtype == GNF4_DTYPE_F16)
-    hipLaunchKernelGGL((k_widen_to_bf16<_Float16>), dim3((unsigned)grid), dim3(256), 0, s,
-                       static_cast<const _Float16*>(src), ld_src, static_cast<uint16_t*>(dst),
+  const bool narrow = rows * vec < (int64_t)0xFFFFFFFF;
+  if (src_dtype == GNF4_DTYPE_F16 && narrow)
+    hipLaunchKernelGGL((k_widen_to_bf16<_Float16, uint32_t>), dim3((unsigned)grid), dim3(256), 0,
+                       s, static_cast<const _Float16*>(src), ld_src, static_cast<uint16_t*>(dst),
+                       ld_dst, (uint32_t)rows, (uint32_t)vec);
+  else if (src_dtype == GNF4_DTYPE_F16)
+    hipLaunchKernelGGL((k_widen_to_bf16<_Float16, int64_t>), dim3((unsigned)grid), dim3(256), 0,
+                       s, static_cast<const _Float16*>(src), ld_src, static_cast<uint16_t*>(dst),
                        ld_dst, rows, vec);
+  else if (narrow)
+    hipLaunchKernelGGL((k_widen_to_bf16<float, uint32_t>), dim3((unsigned)grid), dim3(256), 0, s,
+                       static_cast<const float*>(src), ld_src, static_cast<uint16_t*>(dst),
+                       ld_dst, (uint32_t)rows, (uint32_t)vec);
   else
-    hipLaunchKernelGGL((k_widen_to_bf16<float>), dim3((unsigned)grid), dim3(256), 0, s,
+    hipLaunchKernelGGL((k_widen_to_bf16<float, int64_t>), dim3((unsigned)grid), dim3(256), 0, s,
                        static_cast<const float*>(src), ld_src, static_cast<uint16_t*>(dst),
                        ld_dst, rows, vec);
   return hipGetLastError() == hipSuccess ? 0 : -2;
@@ -2004,9 +2016,14 @@ int gnf4_hip_silu_mul(const void* gu, int64_t ldg, int64_t T, int64_t H, void* h
   if (cus <= 0) return -2;
   const int64_t work = (T * (H / 8) + 255) / 256;
   const int64_t grid = clamp_grid(work, (int64_t)cus * 8);
-  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)grid), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gu), ldg,
-                     static_cast<uint16_t*>(h), ldh, T, H);
+  if (T * (H / 8) < (int64_t)0xFFFFFFFF)
+    hipLaunchKernelGGL((k_silu_mul<uint32_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gu), ldg,
+                       static_cast<uint16_t*>(h), ldh, (uint32_t)T, (uint32_t)H);
+  else
+    hipLaunchKernelGGL((k_silu_mul<int64_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gu), ldg,
+                       static_cast<uint16_t*>(h), ldh, T, H);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -1,0 +1,572 @@
+// gnf4_route.hip -- device-side MoE routing around the grouped 4-bit expert
+// GEMM on MI355X (gfx950): top-k selection with softmax weights, grouping of
+// (token, slot) rows by expert, the gather of activations into group order,
+// and the weighted combine back to token order.
+//
+// With these, a decode MoE layer (router logits -> top-k -> grouped expert
+// FFN -> combine) runs on the device end to end: no host reads of the
+// routing, so a whole layer can be captured in one HIP graph.
+//
+// Reference behaviour followed:
+//   * top-k + softmax weights: gnf4_route_epilogue_bf16,
+//     gnf4_native/cpu_kernels.c:1408-1471 (selection = stable descending sort,
+//     ties to the lower index; mode 0 softmax over all logits gathered at the
+//     selection, optionally renormalised; mode 1 softmax over the selected
+//     logits; weights rounded to bf16 nearest-even);
+//   * grouping, gather and combine: the sort / count / unsort around the
+//     expert matmuls in kernel/arena_moe_patch.py:41-66 (tokens grouped by
+//     expert in ascending expert order, rows of one expert in (token, slot)
+//     order; output = sum over slots of weight * expert output).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/gnf4_hip.h"
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+
+constexpr int kRouteMaxK = 64;        // as the reference's epilogue (bv[64])
+constexpr int kRouteMaxPerLane = 16;  // E <= 1024
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / 64;
+constexpr int kGroupMaxE = 512;
+
+__device__ __forceinline__ uint16_t bf16_rne(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float((uint32_t)b << 16);
+}
+
+// (value, index) order of the selection: larger value first, then lower index.
+__device__ __forceinline__ bool beats(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// Wave-wide reductions on the DPP network: xor-1 and xor-2 quad
+// permutes, the half-row and row mirrors, then row broadcasts 15 and 31
+// carry each row's result into the next rows; lane 63 ends with the whole
+// wave's value, which readlane makes uniform. A fixed sequence, so sums are
+// bitwise reproducible.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140,
+              kDppBcast15 = 0x142, kDppBcast31 = 0x143;
+
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, uint32_t identity, Op op) {
+  const int x = (int)v, id = (int)identity;
+  int t;
+  t = __builtin_amdgcn_update_dpp(id, x, kDppXor1, 0xF, 0xF, false);
+  v = op(v, (uint32_t)t);
+  t = __builtin_amdgcn_update_dpp(id, (int)v, kDppXor2, 0xF, 0xF, false);
+  v = op(v, (uint32_t)t);
+  t = __builtin_amdgcn_update_dpp(id, (int)v, kDppHalfMirror, 0xF, 0xF, false);
+  v = op(v, (uint32_t)t);
+  t = __builtin_amdgcn_update_dpp(id, (int)v, kDppMirror, 0xF, 0xF, false);
+  v = op(v, (uint32_t)t);
+  t = __builtin_amdgcn_update_dpp(id, (int)v, kDppBcast15, 0xA, 0xF, false);
+  v = op(v, (uint32_t)t);
+  t = __builtin_amdgcn_update_dpp(id, (int)v, kDppBcast31, 0xC, 0xF, false);
+  v = op(v, (uint32_t)t);
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return wave_reduce_u32(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return wave_reduce_u32(v, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  const uint32_t r = wave_reduce_u32(__float_as_uint(x), 0u, [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  });
+  return __uint_as_float(r);
+}
+
+// Order-preserving map of a float to u32 (larger float -> larger key; -0
+// and +0 share a key, as they compare equal). Key 0 is below every non-NaN
+// value's key and marks "no candidate".
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u << 1) == 0u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Top-k of one token's logits by one wave. Lane l holds logits l, l + 64,
+// ...; each of the k rounds takes the wave's largest remaining key (DPP max),
+// then the lowest expert index holding it (DPP min): the stable descending
+// order. Lane j < k returns the j-th pick and its weight.
+template <int kPerLane>
+__device__ __forceinline__ void topk_token(const float* __restrict__ lg, int E, int k, int mode,
+                                           int norm, int lane, int& sel_i, float& w) {
+  float v[kPerLane];
+  uint32_t key[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? lg[e] : 0.0f;
+    key[i] = e < E ? order_key(v[i]) : 0u;
+  }
+  // every non-NaN logit has a nonzero key (NaN logits are unspecified input)
+  float sel_v = 0.0f;
+  sel_i = 0;
+  for (int j = 0; j < k; ++j) {
+    uint32_t best = 0u;
+    int best_e = 0x7FFFFFFF;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i)   // ascending e: strict > keeps the lower index
+      if (key[i] > best) {
+        best = key[i];
+        best_e = lane + 64 * i;
+      }
+    const uint32_t top = wave_max_u32(best);
+    const int pick = (int)wave_min_u32(best == top ? (uint32_t)best_e : 0xFFFFFFFFu);
+    float picked = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i)
+      if (lane + 64 * i == pick) {
+        picked = v[i];
+        key[i] = 0u;
+      }
+    // the owner lane (pick % 64) holds the value; broadcast it
+    picked = __uint_as_float((uint32_t)__builtin_amdgcn_readlane(
+        (int)__float_as_uint(picked), pick & 63));
+    if (lane == j) {
+      sel_v = picked;
+      sel_i = pick;
+    }
+  }
+  const bool mine = lane < k;
+  if (mode == 0) {
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i)
+      if (lane + 64 * i < E) m = fmaxf(m, v[i]);
+    m = __uint_as_float(wave_reduce_u32(__float_as_uint(m), __float_as_uint(-__builtin_inff()),
+                                        [](uint32_t a, uint32_t b) {
+                                          return __float_as_uint(fmaxf(__uint_as_float(a),
+                                                                       __uint_as_float(b)));
+                                        }));
+    float z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i)
+      if (lane + 64 * i < E) z += expf(v[i] - m);
+    z = wave_sum(z);
+    w = mine ? expf(sel_v - m) / z : 0.0f;
+    if (norm) w = w / wave_sum(w);
+  } else {
+    const float m = __uint_as_float((uint32_t)__builtin_amdgcn_readlane(
+        (int)__float_as_uint(sel_v), 0));
+    const float ex = mine ? expf(sel_v - m) : 0.0f;
+    w = ex / wave_sum(ex);
+  }
+}
+
+template <int kPerLane>
+__global__ void __launch_bounds__(256) k_route_topk(const float* __restrict__ logits, int64_t ld,
+                                                    int64_t T, int E, int k, int mode, int norm,
+                                                    int64_t* __restrict__ idx,
+                                                    int64_t idx_stride,
+                                                    uint16_t* __restrict__ wts,
+                                                    int64_t wts_stride) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= T) return;   // uniform per wave
+  int sel_i;
+  float w;
+  topk_token<kPerLane>(logits + t * ld, E, k, mode, norm, lane, sel_i, w);
+  if (lane < k) {
+    idx[t * idx_stride + lane] = sel_i;
+    wts[t * wts_stride + lane] = bf16_rne(w);
+  }
+}
+
+// Grouping of N = T * k rows (row i = token i / k, slot i % k) by expert, in
+// one workgroup of 16 waves. Wave w owns the contiguous rows
+// [w * S, (w + 1) * S). (1) per-wave expert counts in LDS; (2) per expert, the
+// waves' exclusive offsets and the expert total; (3) a scan over experts:
+// active experts get consecutive group numbers in ascending expert order;
+// (4) each wave walks its rows in order, 64 at a time, and places the rows of
+// one expert at once (ballot), so rows of an expert stay in row order.
+//
+// Outputs: eids[g], row_off[g] for g < slots (groups past the active count
+// are empty: row_off = N, eids = 0), row_off[slots] = N; order[r] = the row
+// placed at grouped position r; pos[i] = grouped position of row i (-1 for
+// an out-of-range expert id, which is also flagged in info[2]); info[0] =
+// active groups, info[1] = the largest group.
+// `order_lds`, when not null, receives a copy of `order` in LDS.
+__device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_stride, int64_t T,
+                                           int k, int E, int slots, int32_t* __restrict__ eids,
+                                           int32_t* __restrict__ row_off,
+                                           int32_t* __restrict__ order,
+                                           int32_t* __restrict__ pos,
+                                           int32_t* __restrict__ info,
+                                           int32_t* order_lds = nullptr) {
+  __shared__ int32_t s_cnt[kGroupWaves][kGroupMaxE];   // per-wave counts, then cursors
+  __shared__ int32_t s_base[kGroupMaxE];              // first grouped position of expert e
+  __shared__ int32_t s_scan[kGroupThreads];
+  __shared__ int32_t s_scan2[kGroupThreads];
+  __shared__ int32_t s_max, s_bad;
+  // row indices fit in 32 bits (the host checks T * k < 2^31)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int N = (int)(T * k);
+  const int S = (N + kGroupWaves - 1) / kGroupWaves;
+  const int r0 = wave * S, r1 = r0 + S < N ? r0 + S : N;
+  for (int i = tid; i < kGroupWaves * kGroupMaxE; i += kGroupThreads) (&s_cnt[0][0])[i] = 0;
+  if (tid == 0) {
+    s_max = 0;
+    s_bad = 0;
+  }
+  __syncthreads();
+  // (1) counts
+  for (int i = r0 + lane; i < r1; i += 64) {
+    const int64_t e = ids[(int64_t)(i / k) * ids_stride + i % k];
+    if (e >= 0 && e < E)
+      atomicAdd(&s_cnt[wave][e], 1);
+    else
+      s_bad = 1;
+  }
+  __syncthreads();
+  // (2) per expert: exclusive offsets over waves, totals
+  int tot = 0;
+  if (tid < E) {
+    for (int w = 0; w < kGroupWaves; ++w) {
+      const int c = s_cnt[w][tid];
+      s_cnt[w][tid] = tot;
+      tot += c;
+    }
+  }
+  // (3) inclusive scans of totals and of the active flag over experts
+  s_scan[tid] = tid < E ? tot : 0;
+  s_scan2[tid] = tid < E && tot > 0 ? 1 : 0;
+  __syncthreads();
+  for (int off = 1; off < kGroupThreads; off <<= 1) {
+    const int a = tid >= off ? s_scan[tid - off] : 0;
+    const int b = tid >= off ? s_scan2[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += a;
+    s_scan2[tid] += b;
+    __syncthreads();
+  }
+  if (tid < E) {
+    const int base = s_scan[tid] - tot;
+    s_base[tid] = base;
+    if (tot > 0) {
+      const int g = s_scan2[tid] - 1;
+      if (g < slots) {
+        eids[g] = tid;
+        row_off[g] = base;
+      }
+      atomicMax(&s_max, tot);
+    }
+  }
+  const int active = s_scan2[kGroupThreads - 1];
+  for (int g = active + tid; g < slots; g += kGroupThreads) {
+    eids[g] = 0;
+    row_off[g] = (int32_t)N;
+  }
+  if (tid == 0) {
+    row_off[slots] = (int32_t)N;
+    info[0] = active;
+    info[1] = s_max;
+    info[2] = s_bad;
+  }
+  __syncthreads();
+  // (4) stable placement, 64 rows at a time per wave
+  for (int c0 = r0; c0 < r1; c0 += 64) {
+    const int i = c0 + lane;
+    const bool valid = i < r1;
+    int64_t e = valid ? ids[(int64_t)(i / k) * ids_stride + i % k] : -1;
+    const bool ok = valid && e >= 0 && e < E;
+    if (valid && !ok) pos[i] = -1;
+    uint64_t pending = __builtin_amdgcn_ballot_w64(ok);
+    while (pending) {
+      const int leader = __builtin_ctzll(pending);
+      const int le = __shfl((int)e, leader, 64);
+      const uint64_t mask = __builtin_amdgcn_ballot_w64(ok && e == le);
+      const int cur = s_cnt[wave][le];
+      if (ok && e == le) {
+        const int rank = __builtin_popcountll(mask & ((1ull << lane) - 1ull));
+        const int p = s_base[le] + cur + rank;
+        order[p] = (int32_t)i;
+        pos[i] = p;
+        if (order_lds) order_lds[p] = (int32_t)i;
+      }
+      if (lane == leader) s_cnt[wave][le] = cur + __builtin_popcountll(mask);
+      pending &= ~mask;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kGroupThreads) k_route_groups(
+    const int64_t* __restrict__ ids, int64_t ids_stride, int64_t T, int k, int E, int slots,
+    int32_t* __restrict__ eids, int32_t* __restrict__ row_off, int32_t* __restrict__ order,
+    int32_t* __restrict__ pos, int32_t* __restrict__ info) {
+  group_rows(ids, ids_stride, T, k, E, slots, eids, row_off, order, pos, info);
+}
+
+// The whole decode routing prologue in one workgroup (T <= 16 tokens):
+// top-k of each token's logits by one wave (skipped when the caller passes
+// its own ids: logits == nullptr), the grouping, and the gather of the
+// activation rows into group order. The ids and the order stay in LDS
+// between the phases; the gather keeps eight 16-byte loads in flight per
+// thread.
+constexpr int kDecodeMaxRows = kGroupWaves * kRouteMaxK;   // T * k <= 1024
+
+template <int kPerLane>
+__global__ void __launch_bounds__(kGroupThreads) k_route_decode(
+    const float* __restrict__ logits, int64_t ld, int64_t T, int E, int k, int mode, int norm,
+    int64_t* idx, int64_t idx_stride, uint16_t* __restrict__ wts, int64_t wts_stride,
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t K, int slots,
+    int32_t* __restrict__ eids, int32_t* __restrict__ row_off, int32_t* __restrict__ order,
+    int32_t* __restrict__ pos, int32_t* __restrict__ info, uint16_t* __restrict__ a_out,
+    int64_t lda) {
+  __shared__ int64_t s_ids[kDecodeMaxRows];
+  __shared__ int32_t s_order[kDecodeMaxRows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int N = (int)(T * k);
+  if (logits) {
+    if (wave < T) {
+      int sel_i;
+      float w;
+      topk_token<kPerLane>(logits + wave * ld, E, k, mode, norm, lane, sel_i, w);
+      if (lane < k) {
+        idx[wave * idx_stride + lane] = sel_i;
+        wts[wave * wts_stride + lane] = bf16_rne(w);
+        s_ids[wave * k + lane] = sel_i;
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < N; i += kGroupThreads) s_ids[i] = idx[(i / k) * idx_stride + i % k];
+  }
+  __syncthreads();
+  group_rows(s_ids, k, T, k, E, slots, eids, row_off, order, pos, info, s_order);
+  __syncthreads();
+  // 32-bit index math (the host checks T * k * K < 2^31)
+  const int vec = (int)(K / 8), total = N * vec;
+  constexpr int kInFlight = 8;
+  for (int q0 = threadIdx.x; q0 < total; q0 += kInFlight * kGroupThreads) {
+    u32x4_t v[kInFlight];
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const int q = q0 + u * kGroupThreads;
+      if (q < total) {
+        const int r = q / vec, c = (q - r * vec) * 8;
+        v[u] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)(s_order[r] / k) * ldx + c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const int q = q0 + u * kGroupThreads;
+      if (q < total) {
+        const int r = q / vec, c = (q - r * vec) * 8;
+        *reinterpret_cast<u32x4_t*>(a_out + (int64_t)r * lda + c) = v[u];
+      }
+    }
+  }
+}
+
+// out[r, :] = x[order[r] / k, :] for r < N. Eight bf16 per thread. Idx is
+// uint32_t whenever N * K / 8 < 2^32 (64-bit division is a long software
+// sequence on this GPU).
+template <class Idx>
+__global__ void __launch_bounds__(256) k_gather_rows(const uint16_t* __restrict__ x, int64_t ldx,
+                                                     const int32_t* __restrict__ order, Idx N,
+                                                     int k, Idx K, uint16_t* __restrict__ out,
+                                                     int64_t ldo) {
+  const Idx vec = K / 8, total = N * vec;
+  for (Idx q = (Idx)blockIdx.x * blockDim.x + threadIdx.x; q < total;
+       q += (Idx)gridDim.x * blockDim.x) {
+    const Idx r = q / vec, c = (q - r * vec) * 8;
+    const int64_t src = order[r] / k;
+    *reinterpret_cast<u32x4_t*>(out + (int64_t)r * ldo + c) =
+        *reinterpret_cast<const u32x4_t*>(x + src * ldx + c);
+  }
+}
+
+// out[t, d] = bf16(sum_j w[t, j] * y[pos[t * k + j], d]), j ascending, fp32.
+// Rows with pos < 0 (an out-of-range expert id) contribute nothing. Slots go
+// eight at a time: their positions and weights, then their rows, are loaded
+// before any is used.
+template <class Idx>
+__global__ void __launch_bounds__(256) k_route_combine(const uint16_t* __restrict__ y, int64_t ldy,
+                                                       const int32_t* __restrict__ pos,
+                                                       const uint16_t* __restrict__ wts,
+                                                       int64_t wts_stride, Idx T, int k, Idx D,
+                                                       uint16_t* __restrict__ out, int64_t ldo) {
+  const Idx vec = D / 8, total = T * vec;
+  for (Idx q = (Idx)blockIdx.x * blockDim.x + threadIdx.x; q < total;
+       q += (Idx)gridDim.x * blockDim.x) {
+    const int64_t t = q / vec, c = (q - (Idx)t * vec) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      int32_t p[8];
+      float w[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = j0 + jj;
+        p[jj] = j < k ? pos[t * k + j] : -1;
+        w[jj] = j < k ? bf16_to_f32(wts[t * wts_stride + j]) : 0.0f;
+      }
+      u32x4_t v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        v[jj] = p[jj] >= 0 ? *reinterpret_cast<const u32x4_t*>(y + (int64_t)p[jj] * ldy + c)
+                           : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        if (p[jj] < 0) continue;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          acc[2 * h] += w[jj] * __uint_as_float(v[jj][h] << 16);
+          acc[2 * h + 1] += w[jj] * __uint_as_float(v[jj][h] & 0xFFFF0000u);
+        }
+      }
+    }
+    u32x4_t o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      o[h] = (uint32_t)bf16_rne(acc[2 * h]) | ((uint32_t)bf16_rne(acc[2 * h + 1]) << 16);
+    *reinterpret_cast<u32x4_t*>(out + t * ldo + c) = o;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int64_t grid_for(int64_t work_items, int threads) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return -1;
+  const int64_t need = (work_items + threads - 1) / threads;
+  const int64_t cap = (int64_t)cus * 8;
+  return need < 1 ? 1 : (need < cap ? need : cap);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gnf4_hip_route_topk(const float* logits, int64_t T, int64_t E, int64_t ld, int k, int mode,
+                        int norm, int64_t* idx, int64_t idx_stride, uint16_t* wts,
+                        int64_t wts_stride, void* stream) {
+  if (T < 0 || E <= 0 || E > 64 * kRouteMaxPerLane || ld < E || k < 1 || k > kRouteMaxK ||
+      k > E || (mode != 0 && mode != 1) || idx_stride < k || wts_stride < k)
+    return -1;
+  if (T == 0) return 0;
+  if (!logits || !idx || !wts) return -1;
+  const int64_t blocks = (T + 3) / 4;
+  if (blocks > 0x7FFFFFFF) return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int per_lane = (int)((E + 63) / 64);
+#define GNF4_TOPK(P)                                                                        \
+  hipLaunchKernelGGL((k_route_topk<P>), dim3((unsigned)blocks), dim3(256), 0, s, logits, ld, \
+                     T, (int)E, k, mode, norm, idx, idx_stride, wts, wts_stride)
+  if (per_lane <= 1)
+    GNF4_TOPK(1);
+  else if (per_lane <= 2)
+    GNF4_TOPK(2);
+  else if (per_lane <= 4)
+    GNF4_TOPK(4);
+  else if (per_lane <= 8)
+    GNF4_TOPK(8);
+  else
+    GNF4_TOPK(16);
+#undef GNF4_TOPK
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_route_groups(const int64_t* topk_ids, int64_t ids_stride, int64_t T, int k,
+                          int64_t E, int slots, int32_t* eids, int32_t* row_off, int32_t* order,
+                          int32_t* pos, int32_t* info, void* stream) {
+  if (T < 0 || k < 1 || ids_stride < k || E <= 0 || E > kGroupMaxE || slots < 0) return -1;
+  if (T * k > 0x7FFFFFFF) return -1;
+  if (!topk_ids || !eids || !row_off || !order || !pos || !info) return -1;
+  hipLaunchKernelGGL(k_route_groups, dim3(1), dim3(kGroupThreads), 0,
+                     static_cast<hipStream_t>(stream), topk_ids, ids_stride, T, k, (int)E,
+                     slots, eids, row_off, order, pos, info);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_route_decode(const float* logits, int64_t ld, int64_t T, int64_t E, int k,
+                          int mode, int norm, int64_t* idx, int64_t idx_stride, uint16_t* wts,
+                          int64_t wts_stride, const void* x, int64_t ldx, int64_t K, int slots,
+                          int32_t* eids, int32_t* row_off, int32_t* order, int32_t* pos,
+                          int32_t* info, void* a_out, int64_t lda, void* stream) {
+  if (T < 0 || T > kGroupWaves || E <= 0 || E > kGroupMaxE || k < 1 || k > kRouteMaxK ||
+      k > E || idx_stride < k || slots < 0 || K <= 0 || K % 8 || ldx < K || ldx % 8 ||
+      lda < K || lda % 8)
+    return -1;
+  if (logits && (ld < E || (mode != 0 && mode != 1) || !wts || wts_stride < k)) return -1;
+  if (T * k * K >= 0x7FFFFFFF) return -1;   // the gather's 32-bit index math
+  if (!idx || !x || !eids || !row_off || !order || !pos || !info || !a_out || !aligned16(x) ||
+      !aligned16(a_out))
+    return -1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int per_lane = (int)((E + 63) / 64);
+#define GNF4_PRO(P)                                                                           \
+  hipLaunchKernelGGL((k_route_decode<P>), dim3(1), dim3(kGroupThreads), 0, s, logits, ld, T,   \
+                     (int)E, k, mode, norm, idx, idx_stride, wts, wts_stride,                  \
+                     static_cast<const uint16_t*>(x), ldx, K, slots, eids, row_off, order, pos, \
+                     info, static_cast<uint16_t*>(a_out), lda)
+  if (per_lane <= 1)
+    GNF4_PRO(1);
+  else if (per_lane <= 2)
+    GNF4_PRO(2);
+  else if (per_lane <= 4)
+    GNF4_PRO(4);
+  else
+    GNF4_PRO(8);
+#undef GNF4_PRO
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_gather_rows(const void* x, int64_t ldx, const int32_t* order, int64_t N, int k,
+                         int64_t K, void* out, int64_t ldo, void* stream) {
+  if (N < 0 || k < 1 || K <= 0 || K % 8 || ldx < K || ldx % 8 || ldo < K || ldo % 8) return -1;
+  if (N == 0) return 0;
+  if (!x || !order || !out || !aligned16(x) || !aligned16(out)) return -1;
+  const int64_t grid = grid_for(N * (K / 8), 256);
+  if (grid < 0) return -2;
+  if (N * (K / 8) < (int64_t)0xFFFFFFFF)
+    hipLaunchKernelGGL((k_gather_rows<uint32_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), ldx,
+                       order, (uint32_t)N, k, (uint32_t)K, static_cast<uint16_t*>(out), ldo);
+  else
+    hipLaunchKernelGGL((k_gather_rows<int64_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), ldx,
+                       order, N, k, K, static_cast<uint16_t*>(out), ldo);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int gnf4_hip_route_combine(const void* y, int64_t ldy, const int32_t* pos, const uint16_t* wts,
+                           int64_t wts_stride, int64_t T, int k, int64_t D, void* out,
+                           int64_t ldo, void* stream) {
+  if (T < 0 || k < 1 || wts_stride < k || D <= 0 || D % 8 || ldy < D || ldy % 8 || ldo < D ||
+      ldo % 8)
+    return -1;
+  if (T == 0) return 0;
+  if (!y || !pos || !wts || !out || !aligned16(y) || !aligned16(out)) return -1;
+  const int64_t grid = grid_for(T * (D / 8), 256);
+  if (grid < 0) return -2;
+  if (T * (D / 8) < (int64_t)0xFFFFFFFF)
+    hipLaunchKernelGGL((k_route_combine<uint32_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), ldy,
+                       pos, wts, wts_stride, (uint32_t)T, k, (uint32_t)D,
+                       static_cast<uint16_t*>(out), ldo);
+  else
+    hipLaunchKernelGGL((k_route_combine<int64_t>), dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(y), ldy,
+                       pos, wts, wts_stride, T, k, D, static_cast<uint16_t*>(out), ldo);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // extern "C"

@@ -174,27 +174,41 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
         h = silu_mul_locked(gu)
         return nf4_grouped.gemm_4bit_grouped(h, dn_packed, dn_absmax, sizes, expert_ids)
     a = _bf16_activations(a_cat, "gemm_nf4_ffn_grouped")
-    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
-    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
     row_off = [0]
     for m in sizes_i:
         row_off.append(row_off[-1] + m)
     host_eids = [] if eids_dev is not None else expert_ids
     e_h, r_h = to_device_i32((host_eids, row_off), dev)
     eids = eids_dev if eids_dev is not None else e_h
-    h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
+    out = _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, r_h, G, max_m)
+    del e_h, r_h   # the index tensors stay alive until the launch is enqueued
+    return out
+
+
+def _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, row_off, G: int,
+                  max_m: int, h=None, out=None, op="gemm_nf4_ffn_grouped"):
+    """The fused kernel over device group tables (``eids [G]`` and
+    ``row_off [G + 1]`` int32; ``max_m`` an upper bound of the largest group,
+    <= 16). ``a`` bf16 [T, K]."""
+    T, K = a.shape
+    H, n_dn = gu_packed.shape[1] // 2, dn_packed.shape[1]
+    dev = a.device
+    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
+    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
+    if h is None:
+        h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
     sync = _sync_words(dev, G, 2 * H, n_dn)
     with torch.cuda.device(dev):
         rc = _hiplib.load().gnf4_hip_nf4_ffn_fwd(
             a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
             Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
             Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
-            eids.data_ptr(), r_h.data_ptr(), G, max(max_m, 1), 2 * H, K, n_dn,
+            eids.data_ptr(), row_off.data_ptr(), G, max(max_m, 1), 2 * H, K, n_dn,
             h.data_ptr(), h.stride(0), sync.data_ptr(), sync.numel(),
             out.data_ptr(), out.stride(0), _stream_ptr(dev))
-    del e_h, r_h   # the index tensors stay alive until the launch is enqueued
-    _hiplib.check(rc, "gemm_nf4_ffn_grouped")
+    _hiplib.check(rc, op)
     return out
 
 
@@ -210,23 +224,7 @@ def launch_ffn_planned(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, plan, 
     E = gu_packed.shape[0]
     if plan.min_id < 0 or plan.max_id >= E:
         raise ValueError(f"expert id out of range [0, {E})")
-    dev = a_cat.device
     a = _bf16_activations(a_cat, "launch_ffn_planned")
-    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
-    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
-    if h is None:
-        h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    if out is None:
-        out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
-    sync = _sync_words(dev, plan.G, 2 * H, n_dn)
-    with torch.cuda.device(dev):
-        rc = _hiplib.load().gnf4_hip_nf4_ffn_fwd(
-            a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
-            Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
-            Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
-            plan.eids.data_ptr(), plan.row_off.data_ptr(), plan.G, max(plan.max_m, 1), 2 * H,
-            K, n_dn, h.data_ptr(), h.stride(0), sync.data_ptr(), sync.numel(),
-            out.data_ptr(), out.stride(0), _stream_ptr(dev))
-    _hiplib.check(rc, "launch_ffn_planned")
-    return out
+    return _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, plan.eids, plan.row_off,
+                         plan.G, plan.max_m, h=h, out=out, op="launch_ffn_planned")
 

@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 3
+#define GNF4_HIP_ABI_VERSION 4
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -181,6 +181,60 @@ int gnf4_hip_mxfp4_dgrad(const void *grad_out, int g_dtype, int64_t ldg,
                          const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
                          int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
                          void *stream);
+
+/* ---------------------------------------------------------- routing --
+ * Device-side routing around the grouped GEMM, so a decode MoE layer needs
+ * no host read of the routing and can be captured in one graph. */
+
+/* Top-k selection with softmax weights, one token per row of logits
+ * [T, ld] fp32: idx [T, idx_stride] int64 and wts [T, wts_stride] bf16 bits.
+ * GPU counterpart of gnf4_route_epilogue_bf16 (reference
+ * gnf4_native/cpu_kernels.c:1408-1471), same arguments plus ld and stream:
+ * selection in stable-descending order (ties to the lower index); mode 0 =
+ * softmax over all E logits gathered at the selection, renormalised over it
+ * when norm != 0 (olmoe/qwen3); mode 1 = softmax over the k selected logits
+ * (gpt_oss). k <= 64 and k <= E <= 1024. NaN logits: unspecified. */
+int gnf4_hip_route_topk(const float *logits, int64_t T, int64_t E, int64_t ld, int k,
+                        int mode, int norm, int64_t *idx, int64_t idx_stride,
+                        uint16_t *wts, int64_t wts_stride, void *stream);
+
+/* Groups the N = T * k rows (row i = token i / k, slot i % k) of topk_ids
+ * [T, ids_stride] int64 by expert: the sort / count of the reference's MoE
+ * dispatch (kernel/arena_moe_patch.py:41-47), on the device. Active experts
+ * become groups in ascending expert order; rows of one expert keep row
+ * order. Writes eids [slots] int32, row_off [slots + 1] int32 (groups past
+ * the active count are empty), order [N] int32 (grouped position -> row),
+ * pos [N] int32 (row -> grouped position, -1 for an id outside [0, E)),
+ * info [3] int32 (active groups, largest group, 1 if an id was out of
+ * range). E <= 512. slots = min(N, E) holds every case; the tables can be
+ * passed straight to the decode forward / fused FFN with G = slots. */
+int gnf4_hip_route_groups(const int64_t *topk_ids, int64_t ids_stride, int64_t T, int k,
+                          int64_t E, int slots, int32_t *eids, int32_t *row_off,
+                          int32_t *order, int32_t *pos, int32_t *info, void *stream);
+
+/* The decode routing prologue in one launch (T <= 16 tokens, E <= 512):
+ * gnf4_hip_route_topk (skipped when logits is NULL: idx then holds the
+ * caller's ids), gnf4_hip_route_groups and gnf4_hip_gather_rows, with the
+ * same arguments and outputs; a_out [T * k, lda] receives the gathered
+ * rows of x [T, ldx]. */
+int gnf4_hip_route_decode(const float *logits, int64_t ld, int64_t T, int64_t E, int k,
+                          int mode, int norm, int64_t *idx, int64_t idx_stride,
+                          uint16_t *wts, int64_t wts_stride, const void *x, int64_t ldx,
+                          int64_t K, int slots, int32_t *eids, int32_t *row_off,
+                          int32_t *order, int32_t *pos, int32_t *info, void *a_out,
+                          int64_t lda, void *stream);
+
+/* out[r, :] = x[order[r] / k, :] (bf16 rows into grouped order;
+ * reference arena_moe_patch.py:47 `x[idxs // topk]`). K, ldx, ldo % 8 == 0. */
+int gnf4_hip_gather_rows(const void *x, int64_t ldx, const int32_t *order, int64_t N, int k,
+                         int64_t K, void *out, int64_t ldo, void *stream);
+
+/* out[t, :] = bf16(sum_j wts[t, j] * y[pos[t * k + j], :]), j ascending in
+ * fp32 (the reference's unsort + weight + sum, arena_moe_patch.py:59-65).
+ * D, ldy, ldo % 8 == 0. */
+int gnf4_hip_route_combine(const void *y, int64_t ldy, const int32_t *pos,
+                           const uint16_t *wts, int64_t wts_stride, int64_t T, int k,
+                           int64_t D, void *out, int64_t ldo, void *stream);
 
 #ifdef __cplusplus
 }

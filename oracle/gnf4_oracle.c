@@ -330,3 +330,114 @@ ORACLE_EXPORT int gnf4o_ffn_grouped(const float *a, const uint8_t *gu_packed,
     free(h);
     return rc;
 }
+
+/* -------------------------------------------------------------- routing -- */
+
+/* Top-k + softmax weights per token, restating the reference's
+ * gnf4_route_epilogue_bf16 (gnf4_native/cpu_kernels.c:1408-1471): an
+ * insertion selection over ascending e where only a strictly larger value
+ * moves an entry up (ties keep the earlier index = stable descending order);
+ * mode 0: m = max over all logits, z = sum of expf(l - m) in ascending e,
+ * w_j = expf(v_j - m) / z, renormalised by their ascending sum when norm;
+ * mode 1: the same over the k selected values; weights to bf16 by
+ * round-to-nearest-even. Returns -1 on bad arguments. */
+static uint16_t to_bf16_rne(float x) {
+    union { float f; uint32_t u; } v = { x };
+    return (uint16_t)((v.u + 0x7FFFu + ((v.u >> 16) & 1u)) >> 16);
+}
+
+ORACLE_EXPORT int gnf4o_route_topk(const float *logits, int64_t T, int64_t E, int64_t k,
+                                   int mode, int norm, int64_t *idx, uint16_t *wts) {
+    if (k < 1 || k > 64 || k > E || (mode != 0 && mode != 1)) return -1;
+    for (int64_t t = 0; t < T; t++) {
+        const float *lg = logits + t * E;
+        float val[64];
+        int64_t id[64];
+        int64_t n = 0;
+        for (int64_t e = 0; e < E; e++) {
+            float x = lg[e];
+            int64_t slot;
+            if (n < k) {
+                slot = n++;
+            } else if (x > val[k - 1]) {
+                slot = k - 1;
+            } else {
+                continue;
+            }
+            while (slot > 0 && val[slot - 1] < x) {
+                val[slot] = val[slot - 1];
+                id[slot] = id[slot - 1];
+                slot--;
+            }
+            val[slot] = x;
+            id[slot] = e;
+        }
+        float w[64];
+        if (mode == 0) {
+            float m = lg[0];
+            for (int64_t e = 1; e < E; e++)
+                if (lg[e] > m) m = lg[e];
+            float z = 0.0f;
+            for (int64_t e = 0; e < E; e++) z += expf(lg[e] - m);
+            for (int64_t j = 0; j < k; j++) w[j] = expf(val[j] - m) / z;
+            if (norm) {
+                float s = 0.0f;
+                for (int64_t j = 0; j < k; j++) s += w[j];
+                for (int64_t j = 0; j < k; j++) w[j] /= s;
+            }
+        } else {
+            float z = 0.0f;
+            for (int64_t j = 0; j < k; j++) z += expf(val[j] - val[0]);
+            for (int64_t j = 0; j < k; j++) w[j] = expf(val[j] - val[0]) / z;
+        }
+        for (int64_t j = 0; j < k; j++) {
+            idx[t * k + j] = id[j];
+            wts[t * k + j] = to_bf16_rne(w[j]);
+        }
+    }
+    return 0;
+}
+
+/* Grouping of the N = T * k routed rows by expert (the MoE dispatch's
+ * stable sort by expert id, reference kernel/arena_moe_patch.py:41-47):
+ * counts per expert, groups = experts with rows in ascending id order,
+ * row_off = exclusive prefix of the counts, order = rows in (expert, row)
+ * order, pos = its inverse. Returns the number of groups, or -1 for an id
+ * outside [0, E). */
+ORACLE_EXPORT int gnf4o_route_groups(const int64_t *ids, int64_t N, int64_t E, int32_t *eids,
+                                     int32_t *row_off, int32_t *order, int32_t *pos) {
+    int64_t *cnt = (int64_t *)calloc((size_t)E + 1, sizeof(int64_t));
+    if (!cnt) return -2;
+    for (int64_t i = 0; i < N; i++) {
+        if (ids[i] < 0 || ids[i] >= E) {
+            free(cnt);
+            return -1;
+        }
+        cnt[ids[i]]++;
+    }
+    int g = 0;
+    int64_t base = 0;
+    int64_t *start = (int64_t *)malloc(sizeof(int64_t) * (size_t)(E + 1));
+    if (!start) {
+        free(cnt);
+        return -2;
+    }
+    for (int64_t e = 0; e < E; e++) {
+        start[e] = base;
+        if (cnt[e]) {
+            eids[g] = (int32_t)e;
+            row_off[g] = (int32_t)base;
+            g++;
+        }
+        base += cnt[e];
+    }
+    row_off[g] = (int32_t)base;
+    for (int64_t i = 0; i < N; i++) {
+        int64_t p = start[ids[i]]++;
+        order[p] = (int32_t)i;
+        pos[i] = (int32_t)p;
+    }
+    free(start);
+    free(cnt);
+    return g;
+}

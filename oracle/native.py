@@ -64,6 +64,11 @@ def oracle_lib():
         lib.gnf4o_ffn_grouped.restype = ctypes.c_int
         lib.gnf4o_ffn_grouped.argtypes = [_P, _P, _P, _P, _P, _P, _P, ctypes.c_int,
                                           _I64, _I64, _I64, _I64, _P, ctypes.c_int]
+        lib.gnf4o_route_topk.restype = ctypes.c_int
+        lib.gnf4o_route_topk.argtypes = [_P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int,
+                                         _P, _P]
+        lib.gnf4o_route_groups.restype = ctypes.c_int
+        lib.gnf4o_route_groups.argtypes = [_P, _I64, _I64, _P, _P, _P, _P]
         lib.gnf4o_nf4_lut.restype = ctypes.POINTER(ctypes.c_float)
         lib.gnf4o_fp4_lut.restype = ctypes.POINTER(ctypes.c_float)
         _lib = lib
@@ -93,6 +98,9 @@ def ref_lib():
                 lib.gnf4_gemv_nf4_ffn_grouped.argtypes = [
                     _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _I64, _I64, _I64, _P,
                     ctypes.c_int]
+                lib.gnf4_route_epilogue_bf16.restype = None
+                lib.gnf4_route_epilogue_bf16.argtypes = [
+                    _P, _I64, _I64, _I64, ctypes.c_int, ctypes.c_int, _P, _I64, _P, _I64]
                 _ref, _ref_path = lib, path
                 break
     return _ref
@@ -221,6 +229,47 @@ def ref_ffn_grouped(a, gu_packed, gu_absmax, dn_packed, dn_absmax, sizes, expert
     if rc:
         raise ValueError(f"reference ffn rejected the call (rc={rc})")
     return out
+
+
+def route_topk(logits, k, mode, norm):
+    """Oracle top-k + softmax weights: (idx int64 [T, k], wts uint16 bf16 bits)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = lg.shape
+    idx = np.zeros((T, k), dtype=np.int64)
+    wts = np.zeros((T, k), dtype=np.uint16)
+    rc = oracle_lib().gnf4o_route_topk(_ptr(lg), T, E, k, mode, int(norm), _ptr(idx), _ptr(wts))
+    if rc:
+        raise ValueError(f"gnf4o_route_topk rejected the call (rc={rc})")
+    return idx, wts
+
+
+def ref_route_topk(logits, k, mode, norm):
+    """The compiled reference's gnf4_route_epilogue_bf16."""
+    lib = ref_lib()
+    if lib is None:
+        raise RuntimeError("reference build absent (oracle/_ref)")
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = lg.shape
+    idx = np.zeros((T, k), dtype=np.int64)
+    wts = np.zeros((T, k), dtype=np.uint16)
+    lib.gnf4_route_epilogue_bf16(_ptr(lg), T, E, k, mode, int(norm), _ptr(idx), k, _ptr(wts), k)
+    return idx, wts
+
+
+def route_groups(topk_ids, E):
+    """Oracle grouping of the flattened routed rows: (eids, row_off, order,
+    pos) as int32 arrays, eids / row_off over the active groups only."""
+    ids = np.ascontiguousarray(np.asarray(topk_ids, dtype=np.int64).reshape(-1))
+    N = ids.size
+    eids = np.zeros(max(E, 1), dtype=np.int32)
+    row_off = np.zeros(max(E, 1) + 1, dtype=np.int32)
+    order = np.zeros(max(N, 1), dtype=np.int32)
+    pos = np.zeros(max(N, 1), dtype=np.int32)
+    g = oracle_lib().gnf4o_route_groups(_ptr(ids), N, E, _ptr(eids), _ptr(row_off),
+                                        _ptr(order), _ptr(pos))
+    if g < 0:
+        raise ValueError(f"gnf4o_route_groups rejected the call (rc={g})")
+    return eids[:g], row_off[:g + 1], order[:N], pos[:N]
 
 
 def oracle_luts():

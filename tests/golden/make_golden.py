@@ -74,6 +74,23 @@ def ffn_cases():
     }
 
 
+def route_cases():
+    """Router logits in the shape of the reference's epilogue test
+    (kernel/test_cpu_grouped.py:158-188: t=3, e=64, k=8, a three-way tie),
+    plus Qwen3 (E=128, top-8, renormalised) and GPT-OSS (E=32, top-4, softmax
+    over the selection) shapes."""
+    rng = np.random.default_rng(5)
+    tie = rng.standard_normal((3, 64)).astype(np.float32)
+    tie[0, 5] = tie[0, 11] = tie[0, 3]
+    qwen = np.random.default_rng(6).standard_normal((16, 128)).astype(np.float32) * 2
+    oss = np.random.default_rng(7).standard_normal((16, 32)).astype(np.float32) * 3
+    return {
+        "route_tie_mode0": (tie, 8, 0, 0), "route_tie_mode0_norm": (tie, 8, 0, 1),
+        "route_tie_mode1": (tie, 8, 1, 0), "route_qwen3_top8_norm": (qwen, 8, 0, 1),
+        "route_gptoss_top4": (oss, 4, 1, 0),
+    }
+
+
 def main():
     if native.ref_lib() is None:
         raise SystemExit("oracle/_ref is not built (needs the reference tree): make -C oracle")
@@ -111,6 +128,13 @@ def main():
     cases["gemv_nf4_config1_slice"] = ("gemv", "nf4", a8, p8, s8, [4] * 8, list(range(8)))
 
     only = sys.argv[1] if len(sys.argv) > 1 else ""
+    for name, (lg, k, mode, norm) in route_cases().items():
+        if name.startswith(only):
+            idx, wts = native.ref_route_topk(lg, k, mode, norm)
+            np.savez_compressed(HERE / f"{name}.npz", op="route", logits=lg, k=k, mode=mode,
+                                norm=norm, idx=idx, wts=wts,
+                                ref_build=str(native.ref_path().name))
+            print(name, idx.shape)
     for name, args in ffn_cases().items():
         if name.startswith(only):
             x, gu_p, gu_a, dn_p, dn_a, sizes, eids = args

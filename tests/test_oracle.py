@@ -212,7 +212,13 @@ def _golden_cases():
 def test_c_oracle_reproduces_the_reference_golden_vectors(path):
     """Vectors written by the reference's compiled CPU kernels."""
     z = np.load(path)                       # allow_pickle stays False
-    op, fmt = str(z["op"]), str(z["fmt"])
+    op = str(z["op"])
+    if op == "route":
+        k, mode, norm = int(z["k"]), int(z["mode"]), int(z["norm"])
+        idx, wts = native.route_topk(z["logits"], k, mode, norm)
+        assert np.array_equal(idx, z["idx"]) and np.array_equal(wts, z["wts"])
+        return
+    fmt = str(z["fmt"])
     sizes, eids = z["sizes"].tolist(), z["eids"].tolist()
     if op == "ffn":
         args = (z["x"], z["gu_packed"], z["gu_absmax"], z["dn_packed"], z["dn_absmax"],
@@ -229,7 +235,9 @@ def test_golden_set_is_complete():
     names = {p.stem for p in _golden_cases()}
     assert {"gemv_nf4_fixture", "gemv_mxfp4_weird_scales", "dgrad_nf4_fixture",
             "dgrad_mxfp4_weird_scales", "gemv_nf4_config1_slice", "ffn_nf4_groups_1_9_3",
-            "ffn_nf4_single_rows", "ffn_nf4_groups_8_8", "ffn_nf4_silu_clamps"} <= names
+            "ffn_nf4_single_rows", "ffn_nf4_groups_8_8", "ffn_nf4_silu_clamps",
+            "route_tie_mode0", "route_tie_mode0_norm", "route_tie_mode1",
+            "route_qwen3_top8_norm", "route_gptoss_top4"} <= names
 
 
 needs_ref = pytest.mark.skipif(native.ref_lib() is None, reason="oracle/_ref not built here")
@@ -395,3 +403,62 @@ def _ffn_case(seed, sizes, scale=1.0):
 def test_ffn_oracle_equals_the_compiled_reference_live(sizes, scale):
     args = _ffn_case(40 + len(sizes), sizes, scale)
     assert np.array_equal(native.ffn_grouped(*args), native.ref_ffn_grouped(*args))
+
+
+# ---------------------------------------------------------------- routing --
+
+@pytest.mark.parametrize("t,e,k", [(3, 64, 8), (40, 128, 8), (25, 32, 4), (5, 300, 64)])
+def test_route_selection_is_the_stable_descending_sort(t, e, k):
+    rng = np.random.default_rng(t + e)
+    lg = rng.standard_normal((t, e)).astype(np.float32)
+    lg[0, 2] = lg[0, 7] = lg[0, 1]                       # ties
+    lg[1, :] = 0.5                                       # all equal
+    for mode, norm in ((0, 0), (0, 1), (1, 0)):
+        idx, wts = native.route_topk(lg, k, mode, norm)
+        assert np.array_equal(idx, np.argsort(-lg, axis=-1, kind="stable")[:, :k])
+
+
+def test_route_weights_follow_the_softmax_closed_forms():
+    rng = np.random.default_rng(9)
+    lg = (rng.standard_normal((30, 128)) * 3).astype(np.float32)
+    k = 8
+    order = np.argsort(-lg, axis=-1, kind="stable")[:, :k]
+    top = np.take_along_axis(lg, order, -1).astype(np.float64)
+    full = np.exp(lg - lg.max(-1, keepdims=True))
+    full = full / full.sum(-1, keepdims=True)
+    sel = np.take_along_axis(full, order, -1)
+    want = {(0, 0): sel, (0, 1): sel / sel.sum(-1, keepdims=True),
+            (1, 0): np.exp(top - top[:, :1]) / np.exp(top - top[:, :1]).sum(-1, keepdims=True)}
+    for (mode, norm), w in want.items():
+        _idx, wts = native.route_topk(lg, k, mode, norm)
+        got = (wts.astype(np.uint32) << 16).view(np.float32)
+        np.testing.assert_allclose(got, w, rtol=8e-3, atol=1e-6)
+
+
+@needs_ref
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_route_topk_equals_the_compiled_reference_live(seed):
+    rng = np.random.default_rng(seed)
+    lg = (rng.standard_normal((33, 128)) * (1 + seed)).astype(np.float32)
+    lg[3, 10] = lg[3, 20] = lg[3, 30]
+    for k, mode, norm in ((8, 0, 1), (8, 0, 0), (4, 1, 0), (64, 0, 1)):
+        a = native.route_topk(lg, k, mode, norm)
+        b = native.ref_route_topk(lg, k, mode, norm)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_route_groups_is_the_stable_sort_by_expert():
+    rng = np.random.default_rng(4)
+    for T, k, E in ((1, 8, 128), (16, 8, 128), (300, 4, 32), (7, 2, 3)):
+        ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+        eids, row_off, order, pos = native.route_groups(ids, E)
+        flat = ids.reshape(-1)
+        want_order = np.argsort(flat, kind="stable")
+        assert np.array_equal(order, want_order)
+        assert np.array_equal(pos[order], np.arange(flat.size))
+        counts = np.bincount(flat, minlength=E)
+        assert np.array_equal(eids, np.nonzero(counts)[0])
+        assert np.array_equal(np.diff(row_off), counts[counts > 0])
+        assert row_off[0] == 0 and row_off[-1] == flat.size
+    with pytest.raises(ValueError):
+        native.route_groups(np.array([[0, 5]]), 4)

@@ -1095,7 +1095,7 @@ __global__ void __launch_bounds__(512, 2)
   // MFMAs of step f (slot r) over the first kM activation subtiles. The
   // weights are operand A, so acc[i] holds out^T: lane (l32, h) gets token
   // row i * 32 + l32 and columns 8 g + 4 h + (0..3), g = 0..3.
-  auto mma = [&](auto RI, auto MI, const char* stage) {
+  auto mma = [&](auto RI, auto MI, const char* stage, auto&& after_first) {
     constexpr int r = decltype(RI)::value;
     constexpr int kM = decltype(MI)::value;
     // operands of k-slices kk and kk + 1 in flight; the reads for kk + 2 go
@@ -1117,6 +1117,10 @@ __global__ void __launch_bounds__(512, 2)
         acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[r & 1][kk]),
                                                           as_bf16x8(av[kk & 1][i]), acc[i], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
+      if (kk == 0) {
+        after_first();
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (kk + 2 < 4) read(kk & 1, kk + 2);
     }
   };
@@ -1126,25 +1130,25 @@ __global__ void __launch_bounds__(512, 2)
   // reverse -- so while one wave decodes on the VALU the other keeps the
   // matrix core busy. The order is a template argument of the whole loop
   // (each wave half runs its own copy), so no step merges two orders.
-  auto mma_decode = [&](auto RI, auto MI, auto DF, const char* stage) {
+  auto mma_decode = [&](auto RI, auto MI, auto DF, const char* stage, auto&& after_first) {
     constexpr int r = decltype(RI)::value;
     if constexpr (decltype(DF)::value) {
       decode(std::integral_constant<int, (r + 1) % kS>{});
       __builtin_amdgcn_sched_barrier(0);
-      mma(RI, MI, stage);
+      mma(RI, MI, stage, after_first);
     } else {
-      mma(RI, MI, stage);
+      mma(RI, MI, stage, after_first);
       __builtin_amdgcn_sched_barrier(0);
       decode(std::integral_constant<int, (r + 1) % kS>{});
     }
   };
 
-  auto compute = [&](auto RI, auto DF, const char* stage) {
+  auto compute = [&](auto RI, auto DF, const char* stage, auto&& after_first) {
     constexpr int r = decltype(RI)::value;
     const int rows = uniform(ring_t[r].rows);
     // every tile runs all 4 subtiles (rows past the group are zeros in LDS):
     // one straight-line step keeps the accumulators in place
-    mma_decode(RI, std::integral_constant<int, 4>{}, DF, stage);
+    mma_decode(RI, std::integral_constant<int, 4>{}, DF, stage, after_first);
     if (ring_last[r]) {
       const PfTile t = ring_t[r];
       const int n_l = t.n0 + wave * kWaveCols + 4 * h;   // lane's first column
@@ -1166,8 +1170,9 @@ __global__ void __launch_bounds__(512, 2)
   };
 
   // Step f: wait for stage f (loads issued after it: the kS - 2 younger
-  // stages), barrier, refill the stage read in step f - 1 with step
-  // f + kS - 1, compute.
+  // stages), barrier, compute; the refill of the stage read in step f - 1
+  // with step f + kS - 1 goes out after the first k-slice's MFMAs, so the
+  // eight waves' loads do not queue up behind the barrier all at once.
   int f = 0;
   auto step = [&](auto RI, auto DF) {
     constexpr int r = decltype(RI)::value;
@@ -1176,10 +1181,10 @@ __global__ void __launch_bounds__(512, 2)
     wait_vm_lgkm0<(kS - 2) * kGroupLoads>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}),
-          f + kS - 1 < F);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(RI, DF, stage_of(RI));
+    const bool live = f + kS - 1 < F;
+    compute(RI, DF, stage_of(RI), [&]() {
+      issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}), live);
+    });
     return ++f < F;
   };
 
@@ -1196,6 +1201,257 @@ __global__ void __launch_bounds__(512, 2)
     auto st = [&](auto RI) { return step(RI, std::false_type{}); };
     while (StepUnroll<0, kS>::run(st)) {
     }
+  }
+}
+
+// Tall variant of k_prefill: 256-row tiles. The decoded weights of a step
+// (each lane: 32 k of one weight row, decoded once) feed eight 32-row
+// activation subtiles instead of four, so the VALU decode per MFMA halves --
+// on gfx950 the VALU and the matrix core barely overlap within a SIMD, which
+// makes decode VALU per MFMA the step's second cost after the MFMAs. A tile
+// of at most 128 rows (a group's tail) runs only the lower four subtiles.
+// LDS: the NF4 pair table (64 KiB, static, so its base folds into the
+// instructions' offset field) and three 32 KiB activation stages; kS = 3, so
+// the step loop unrolls over six steps to keep the decode double buffer's
+// parity static.
+constexpr int kPtBM = 256;
+constexpr int kPtStage = kPtBM * kPfBK * 2;
+
+template <int FMT>
+__global__ void __launch_bounds__(512, 2)
+    k_prefill_t(const FwdArgs p, const int32_t* __restrict__ t_row0,
+                const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
+                const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
+  constexpr int kS = 3;
+  constexpr int kWaves = 8;
+  constexpr int kWaveCols = kPfBN / kWaves;          // 32
+  constexpr int kAPieces = kPtStage / 1024 / kWaves; // 4
+  constexpr int kRowsPerWave = kPtBM / kWaves;       // 32
+  constexpr int kGroupLoads = kAPieces + 2;
+  constexpr int kMT = kPtBM / 32;                    // 8
+  static_assert(kWaveCols == 32, "one weight subtile per wave");
+  __shared__ __attribute__((aligned(16))) float2 s_tab[FMT == kNF4 ? kPairEntries : 2];
+  __shared__ __attribute__((aligned(16))) char s_a0[kPtStage];
+  __shared__ __attribute__((aligned(16))) char s_a1[kPtStage];
+  __shared__ __attribute__((aligned(16))) char s_a2[kPtStage];
+  auto stage_of = [&](auto RI) -> char* {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (r == 0) return s_a0;
+    else if constexpr (r == 1) return s_a1;
+    else return s_a2;
+  };
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);
+  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const unsigned lane_off = (unsigned)(lane & 31) * 8u;
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+
+  const int n_tiles = (int)((p.N + kPfBN - 1) / kPfBN);
+  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
+  const int nx = gridDim.x >= 8 ? 8 : 1;
+  const int x = (int)(blockIdx.x % nx), slot = (int)(blockIdx.x / nx);
+  const int wpx = (int)((gridDim.x - x + nx - 1) / nx);
+  const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
+  const int my_tiles = lo + slot < hi ? (int)((hi - lo - slot + wpx - 1) / wpx) : 0;
+  const int ksteps = (int)((p.K + kPfBK - 1) / kPfBK);
+  const int F = my_tiles * ksteps;
+  if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
+  if (F == 0) return;
+
+  auto meta = [&](int j) {
+    PfTile t;
+    const int64_t tg = lo + slot + (int64_t)j * wpx;
+    const int mt = (int)(tg / n_tiles);
+    t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
+    t.row0 = t_row0[mt];
+    t.rows = t_rows[mt];
+    t.e = eids[t_group[mt]];
+    return t;
+  };
+
+  const int64_t lda2 = p.lda * 2;
+  int a_row[kAPieces], a_slot[kAPieces];
+#pragma unroll
+  for (int i = 0; i < kAPieces; ++i) {
+    a_row[i] = wave * kRowsPerWave + i * 8 + (lane >> 3);
+    a_slot[i] = (lane & 7) ^ pf_swz(a_row[i] & 15);
+  }
+  int a_off[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) a_off[kk] = l32 * 128 + ((4 * h + kk) ^ pf_swz(l32 & 15)) * 16;
+
+  u32x4_t wreg[kS];
+  unsigned sreg[kS];
+  PfTile ring_t[kS];
+  bool ring_last[kS];
+  f32x16_t acc[kMT];
+#pragma unroll
+  for (int i = 0; i < kMT; ++i) acc[i] = f32x16_t{};
+
+  int iss_j = 0, iss_ks = 0;
+  PfTile iss_t;
+  const char* a_base = nullptr;
+  const uint8_t* b_base = nullptr;
+  const char* s_base = nullptr;
+  int a_bytes = 0, b_bytes = 0, s_bytes = 0;
+  int a_voff[kAPieces], b_voff = 0, s_voff = 0;
+  auto tile_setup = [&](int j) {
+    iss_t = meta(j);
+    a_base = reinterpret_cast<const char*>(p.a + (int64_t)iss_t.row0 * p.lda);
+    a_bytes = (int)((int64_t)iss_t.rows * lda2);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      a_voff[i] = a_row[i] < iss_t.rows ? (int)(a_row[i] * lda2) + a_slot[i] * 16 : kOOB;
+    b_base = p.B + (int64_t)iss_t.e * p.sbe;
+    b_bytes = (int)(p.N * p.sbn);
+    s_base = static_cast<const char*>(p.S) + (int64_t)iss_t.e * p.sse * kScaleBytes;
+    s_bytes = (int)(p.N * p.ssn * kScaleBytes);
+    const int64_t n = iss_t.n0 + wave * kWaveCols + l32;
+    b_voff = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
+    if constexpr (FMT == kNF4) s_voff = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
+    else s_voff = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+  };
+  tile_setup(0);
+
+  auto issue = [&](auto RI, char* stage, bool live) {
+    constexpr int r = decltype(RI)::value;
+    const int k0 = uniform(iss_ks) * kPfBK;
+    live = uniform(live ? 1 : 0) != 0;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a_base), 0, uniform(live ? a_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < kAPieces; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (lds_ptr_t)(stage + (wave * kAPieces + i) * 1024), 16, a_voff[i], k0 * 2, 0, 0);
+    wreg[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, b_voff, k0 >> 1, 0));
+    if constexpr (FMT == kNF4)
+      sreg[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff, (k0 >> 6) * 4, 0);
+    else
+      sreg[r] = __builtin_amdgcn_raw_buffer_load_b8(rs, s_voff, k0 >> 5, 0);
+    ring_t[r] = iss_t;
+    ring_last[r] = iss_ks == ksteps - 1;
+    if (++iss_ks == ksteps) {
+      iss_ks = 0;
+      ++iss_j;
+      if (iss_j < my_tiles) tile_setup(iss_j);
+    }
+  };
+
+  // wf: the current step's decoded operands; the next step's are decoded
+  // into the same registers once this step's MFMAs have issued.
+  u32x4_t wf[4];
+  auto decode = [&](auto RI) {
+    constexpr int r = decltype(RI)::value;
+    if constexpr (FMT == kNF4) {
+      const float sc = __uint_as_float(sreg[r]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) wf[kk] = nf4_dword_to_bf16(s_tab, wreg[r][kk], lane_off, sc);
+    } else {
+      const float sc = e8m0_to_f32(sreg[r]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) wf[kk] = mx_dword_to_bf16(wreg[r][kk], sc);
+    }
+  };
+
+  // MFMAs of a step over the first kM activation subtiles (parity q's
+  // weights); the first k-slice's MFMAs are followed by `after_first`.
+  // One operand register per subtile: subtile i's operand for slice kk + 1
+  // is read right after slice kk's MFMA on it issues, and the slice's
+  // remaining MFMAs cover the LDS latency. `full` == false (a tail tile of at
+  // most 128 rows) skips the upper four subtiles; only their MFMAs and reads
+  // sit under the (uniform) branch.
+  auto mma = [&](bool full, const char* stage, auto&& after_first) {
+    constexpr int kHalf = kMT / 2;
+    u32x4_t av[kMT];
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i)
+      av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[0] + i * 4096);
+    if (full) {
+#pragma unroll
+      for (int i = kHalf; i < kMT; ++i)
+        av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[0] + i * 4096);
+    }
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int i = 0; i < kHalf; ++i) {
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[kk]), as_bf16x8(av[i]),
+                                                          acc[i], 0, 0, 0);
+        if (kk + 1 < 4)
+          av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk + 1] + i * 4096);
+      }
+      if (full) {
+#pragma unroll
+        for (int i = kHalf; i < kMT; ++i) {
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[kk]), as_bf16x8(av[i]),
+                                                            acc[i], 0, 0, 0);
+          if (kk + 1 < 4)
+            av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk + 1] + i * 4096);
+        }
+      }
+      if (kk == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        after_first();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  auto compute = [&](auto RI, const char* stage, auto&& after_first) {
+    constexpr int r = decltype(RI)::value;
+    constexpr int rn = (r + 1) % kS;
+    const int rows = uniform(ring_t[r].rows);
+    // a tail tile of at most 128 rows skips the upper four subtiles
+    mma(rows > kPtBM / 2, stage, after_first);
+    __builtin_amdgcn_sched_barrier(0);
+    decode(std::integral_constant<int, rn>{});
+    if (ring_last[r]) {
+      const PfTile t = ring_t[r];
+      const int n_l = t.n0 + wave * kWaveCols + 4 * h;
+      uint16_t* o = out + (int64_t)(t.row0 + l32) * p.ldo + n_l;
+#pragma unroll
+      for (int i = 0; i < kMT; ++i) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if (i * 32 + l32 < rows && n_l + 8 * g < p.N) {
+            uint2 v;
+            v.x = bf16x2_bits(acc[i][4 * g + 0], acc[i][4 * g + 1]);
+            v.y = bf16x2_bits(acc[i][4 * g + 2], acc[i][4 * g + 3]);
+            *reinterpret_cast<uint2*>(o + (int64_t)i * 32 * p.ldo + 8 * g) = v;
+          }
+        }
+        acc[i] = f32x16_t{};
+      }
+    }
+  };
+
+  // Step f uses ring slot f % 3.
+  int f = 0;
+  auto step = [&](auto RI) {
+    constexpr int r = decltype(RI)::value;
+    constexpr int rf = (r + kS - 1) % kS;
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm_lgkm0<(kS - 2) * kGroupLoads>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    const bool live = f + kS - 1 < F;
+    compute(RI, stage_of(RI), [&]() {
+      issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}), live);
+    });
+    return ++f < F;
+  };
+
+  issue(std::integral_constant<int, 0>{}, s_a0, true);
+  issue(std::integral_constant<int, 1>{}, s_a1, F > 1);
+  if constexpr (FMT == kNF4) __syncthreads();  // pair table complete
+  decode(std::integral_constant<int, 0>{});
+  auto st = [&](auto RI) { return step(RI); };
+  while (StepUnroll<0, kS>::run(st)) {
   }
 }
 
@@ -1836,8 +2092,16 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
     if (rc) return rc;
   } else {
     const bool pf_ok = p.N % 4 == 0 && p.ldo % 4 == 0 && p.K % kPfBK == 0 &&
-                       (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
-                       (int64_t)kPfBM * p.lda * 2 < 0x7FFFFFFF;
+                       (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPtBM &&
+                       (int64_t)kPtBM * p.lda * 2 < 0x7FFFFFFF;
+    if (pf_ok && prefill_enabled() && block_m == kPtBM) {
+      const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
+      const int64_t grid = tiles < cus ? tiles : cus;
+      hipLaunchKernelGGL((k_prefill_t<FMT>), dim3((unsigned)grid), dim3(512), 0, stream, p,
+                         p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+      return hipGetLastError() == hipSuccess ? 0 : -2;
+    }
+    if (block_m > kPfBM) return -1;
     if (pf_ok && prefill_enabled()) {
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
       int64_t grid = tiles < cus ? tiles : cus;

@@ -331,7 +331,7 @@ def _prefill_block_m(max_rows: int) -> int:
     return 128
 
 
-_SUPPORTED_BLOCK_M = (16, 32, 64, 128)
+_SUPPORTED_BLOCK_M = (16, 32, 64, 128, 256)
 
 
 def _kernel_block_m(block_m: int) -> int:
@@ -341,6 +341,14 @@ def _kernel_block_m(block_m: int) -> int:
         if block_m <= bm:
             return bm
     return 128
+
+
+def _auto_block_m(max_rows: int) -> int:
+    """Tile height the forward uses when the caller names none: the
+    reference's group-size rule (``_prefill_block_m``), except that groups of
+    more than 128 rows take the 256-row tiles of the tall MFMA kernel (each
+    decoded weight then feeds twice the rows; the bits are the same)."""
+    return 256 if max_rows > 128 else _kernel_block_m(_prefill_block_m(max_rows))
 
 
 # ------------------------------------------------------------------ launch --
@@ -442,8 +450,8 @@ class GroupPlan:
             self.tables = None
             self.block_m = self.max_m
         else:
-            self.block_m = _kernel_block_m(block_m if block_m is not None
-                                           else _prefill_block_m(self.max_m))
+            self.block_m = (_kernel_block_m(block_m) if block_m is not None
+                            else _auto_block_m(self.max_m))
             t0, tr, tg = _tiles_host(sizes_i, self.block_m)
             self.eids = torch.tensor(ids, dtype=torch.int32, device=dev)
             self.row_off = None
@@ -516,7 +524,7 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
         # decode path: block_m carries the largest group size
         args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, max_m)
     else:
-        bm = _kernel_block_m(block_m if block_m is not None else _prefill_block_m(max_m))
+        bm = _kernel_block_m(block_m) if block_m is not None else _auto_block_m(max_m)
         t0, tr, tg = _tiles_host(sizes_i, bm)
         e_h, t0_d, tr_d, tg_d = to_device_i32((host_eids, t0, tr, tg), dev)
         eids = eids_dev if eids_dev is not None else e_h

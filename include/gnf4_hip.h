@@ -30,7 +30,10 @@
  *   n_mtiles  > 0 -> tiled path: the tile table t_row0/t_rows/t_group
  *                    [n_mtiles] int32 (reference build_group_tiles,
  *                    kernel/nf4_grouped.py:334-362) with block_m in
- *                    {16, 32, 64, 128}; t_rows[i] <= block_m.
+ *                    {16, 32, 64, 128, 256}; t_rows[i] <= block_m. 256
+ *                    (forward only) selects the tall MFMA kernel and needs
+ *                    K % 64 == 0, N % 4 == 0, ldo % 4 == 0 and an 8-byte
+ *                    aligned out (-1 otherwise).
  *
  * Return codes (the reference CPU tier's convention, gnf4_native/cpu_kernels.c:745-761):
  *   0 success, -1 shape or argument violation, -2 launch error.

@@ -326,3 +326,21 @@ def test_planned_launch_matches_the_op_and_replays_in_a_graph(fmt):
             g.replay()
             torch.cuda.synchronize()
             assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("sizes", [[300, 17, 129, 256, 1, 600], [257], [128, 130]])
+def test_tall_tiles_give_the_bits_of_128_row_tiles(fmt, sizes):
+    """256-row tiles (the default above 128 rows) change how rows are
+    batched, never an output's arithmetic: bitwise equal to 128-row tiles,
+    tail tiles of <= 128 rows included."""
+    N, K = 512, 1024
+    W, S = _stack(fmt, 8, N, K, seed=61)
+    ids = list(range(len(sizes)))
+    a = rand_acts(sum(sizes), K, seed=62)
+    op = _ops()[fmt]
+    tall = op(a, W, S, sizes, ids, block_m=256)
+    short = op(a, W, S, sizes, ids, block_m=128)
+    auto = op(a, W, S, sizes, ids)
+    assert torch.equal(tall, short) and torch.equal(auto, tall)
+    contract_check(fmt, tall, a, W, S, sizes, ids)

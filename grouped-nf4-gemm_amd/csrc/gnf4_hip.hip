@@ -60,6 +60,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
 
 constexpr int kNF4 = GNF4_FMT_NF4;
 constexpr int kMX = GNF4_FMT_MXFP4;
@@ -1455,25 +1456,6 @@ __global__ void __launch_bounds__(512, 2)
   }
 }
 
-// ========================================================== tiled dgrad ==
-//
-// out[t, k] = sum_n grad[t, n] W[e][n, k]: the weights are read transposed.
-// Same skeleton as k_prefill -- 128-row tiles of one group x 256 output
-// columns (here: k), a persistent XCD-contiguous tile list, a 4-stage ring of
-// gradient rows filled by direct-to-LDS loads, one flat pipeline over (tile,
-// 64-wide n-step) -- with the weight operand going through LDS:
-//   * per step each thread loads 4 packed rows (n) x 8 columns (k) -- one
-//     dword per row -- decodes them and writes them transposed (k-major, 4
-//     consecutive n per 8-byte write) into a double-buffered bf16 tile of 256
-//     k-rows x 64 n, decoded during the step before the one that reads it;
-//   * wave w reads its 32 k-rows of that tile as MFMA operand A and the
-//     gradient rows from the stage as operand B (32 x 32 x 16 bf16).
-// The NF4 pair table here has 16 lane columns (32 KiB), so stages, weight
-// tiles and table fit the 160 KiB of LDS.
-constexpr int kDgTile = kPfBN;            // output columns (k) per tile
-constexpr int kDgStep = 64;               // n per step
-constexpr int kDgBStage = kDgTile * kDgStep * 2;
-
 // Pair table with 16 columns: entry (byte b, column c) at b * 128 + c * 8.
 __device__ __forceinline__ void init_pair_table16(float2* tab, int lut) {
   const unsigned b = threadIdx.x & 255;
@@ -1498,6 +1480,384 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
   }
   return r;
 }
+
+// ==================================================== four-wave prefill ==
+//
+// k_prefill_w<FMT>: the tall-tile forward (256 token rows of one group x 256
+// weight rows per tile), one tile per 256-thread workgroup, one workgroup per
+// CU and one wave per SIMD. Each wave owns 64 weight rows (two 32-row MFMA
+// blocks) for all 256 token rows, so
+//   * every activation operand read from LDS feeds two MFMAs (half the LDS
+//     operand traffic of a 32-row-per-wave split), and
+//   * a wave has the whole register file: 256 accumulator registers and room
+//     to decode the next step's weights while this step's MFMAs run.
+// Everything a step touches comes through LDS rings filled by direct-to-LDS
+// loads two steps ahead (activation stages, and per wave the packed weight
+// bytes and scales), so the step loop is not unrolled over ring slots and
+// the accumulators keep fixed registers.
+// The decode of a k-slice is interleaved with the MFMAs of the following
+// slice ("rolling" decode): during slice 0 of step f the wave decodes slice 3
+// of step f, during slices 1..3 it decodes slices 0..2 of step f + 1, each
+// into the operand registers the previous slice's MFMAs released.
+// One tile per workgroup: the hardware dispatcher hands the next tile to
+// whichever CU frees first, which balances ragged tiles. Tile ids are ordered
+// so each XCD (workgroup ids go to the XCDs round robin) works through a
+// contiguous range of the m-tile-major tile list.
+// The k order of every output element is that of k_prefill / k_prefill_t, so
+// all three give identical bits. Tiles of at most 128 or 64 rows skip the
+// MFMAs and operand reads of their empty 32-row subtiles.
+//
+// LDS map: activation stages at 0, 32 and 64 KiB; weight ring at 96 KiB
+// (three 10 KiB slots: 8 KiB of packed bytes, then the scales); the 16-column
+// NF4 pair table at 128 KiB.
+constexpr int kPwWaves = 4;
+constexpr int kPwRowsPerWave = kPtBM / kPwWaves;           // 64 activation rows staged per wave
+constexpr int kPwAPieces = kPtStage / 1024 / kPwWaves;     // 8 direct-to-LDS loads per wave
+constexpr int kPwGroupLoads = kPwAPieces + 4;              // + 2 weight + 2 scale loads
+constexpr int kPwW0 = 3 * kPtStage;                        // weight ring
+constexpr int kPwWSlot = 10 * 1024;                     // 8 KiB packed bytes + 4 waves x 2 x 256 B scales
+constexpr int kPwTab = 0x20000;                            // 16-column pair table
+constexpr int kPwLds = kPwTab + 256 * 16 * 8;              // 160 KiB
+static_assert(kPwW0 + 3 * kPwWSlot <= kPwTab, "weight ring below the pair table");
+
+template <int FMT, int kM>
+__device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t, char* smem,
+                                               uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+  const int F = (int)((p.K + kPfBK - 1) / kPfBK);
+  // table address << 1 | column * 16 (nf4_dword_to_bf16_t16)
+  const unsigned reg2 = ((unsigned)kPwTab << 1) | (unsigned)(lane & 15) * 16u;
+
+  // k mapping within a 64-wide step (as in k_prefill): lane half h covers
+  // k [32 h, 32 h + 32); MFMA slice kk takes k [32 h + 8 kk, +8).
+  int a_off[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) a_off[kk] = l32 * 128 + ((4 * h + kk) ^ pf_swz(l32 & 15)) * 16;
+
+  // ---- per-tile load descriptors: rows and columns outside the tile fold
+  // into out-of-range offsets; per step only the k offset (soffset) moves
+  const char* a_base = reinterpret_cast<const char*>(p.a + (int64_t)t.row0 * p.lda);
+  const int a_bytes = (int)((int64_t)t.rows * p.lda * 2);
+  int a_voff[kPwAPieces];
+#pragma unroll
+  for (int i = 0; i < kPwAPieces; ++i) {
+    // staged row wave * 64 + 8 i + lane / 8, 16-byte slot (lane % 8) ^ swizzle
+    const int row = wave * kPwRowsPerWave + i * 8 + (lane >> 3);
+    const int slot16 = (lane & 7) ^ pf_swz(row & 15);
+    a_voff[i] = row < t.rows ? (int)(row * p.lda * 2) + slot16 * 16 : kOOB;
+  }
+  const uint8_t* b_base = p.B + (int64_t)t.e * p.sbe;
+  const char* s_base = static_cast<const char*>(p.S) + (int64_t)t.e * p.sse * kScaleBytes;
+  const int b_bytes = (int)(p.N * p.sbn);
+  const int s_bytes = (int)(p.N * p.ssn * kScaleBytes);
+  int b_voff[2], s_voff[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int64_t n = t.n0 + wave * 64 + rb * 32 + l32;
+    b_voff[rb] = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
+    if constexpr (FMT == kNF4) s_voff[rb] = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
+    else s_voff[rb] = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+  }
+  // this wave's blocks of a weight slot: bytes (rb) at +rb KiB, lane-linear;
+  // scales one dword per lane (direct-to-LDS loads of a byte still land in
+  // a dword slot per lane)
+  const int w_wave = (wave * 2) * 1024;
+  const int s_wave = 8192 + (wave * 2) * 256;
+
+  // issue step g's loads: activation stage g % 3, weight slot g % 3 (zero-size
+  // resources past the end, so every step issues the same loads and the
+  // vector-memory counts hold)
+  // Loads are issued in parts (so a slice never issues more than a few):
+  // activation pieces [p0, p1) of step g, and weight loads [q0, q1) of step g
+  // (0, 1: packed bytes of row blocks 0, 1; 2, 3: their scales).
+  auto issue_a = [&](int g, int p0, int p1) {
+    const bool live = g < F;
+    const int k0 = live ? g * kPfBK : 0;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a_base), 0, uniform(live ? a_bytes : 0), 0x00020000);
+    char* stage = smem + uniform((g % 3) * kPtStage) + wave * kPwAPieces * 1024;
+#pragma unroll
+    for (int i = 0; i < kPwAPieces; ++i)
+      if (i >= p0 && i < p1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(stage + i * 1024), 16, a_voff[i],
+                                                 uniform(k0 * 2), 0, 0);
+  };
+  auto issue_w = [&](int g, int q0, int q1) {
+    const bool live = g < F;
+    const int k0 = live ? g * kPfBK : 0;
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
+    char* slot = smem + kPwW0 + uniform((g % 3) * kPwWSlot);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+      if (b >= q0 && b < q1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(slot + w_wave + b * 1024), 16,
+                                                 b_voff[b], uniform(k0 >> 1), 0, 0);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if (b + 2 < q0 || b + 2 >= q1) continue;
+      if constexpr (FMT == kNF4)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave + b * 256), 4,
+                                                 s_voff[b], uniform((k0 >> 6) * 4), 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave + b * 256), 1,
+                                                 s_voff[b], uniform(k0 >> 5), 0, 0);
+    }
+  };
+  // this lane's packed bytes and scale of step g (block rb), from its slot
+  auto read_w = [&](int g, u32x4_t (&w)[2], float (&sc)[2]) {
+    const char* slot = smem + kPwW0 + uniform((g % 3) * kPwWSlot);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      w[b] = *reinterpret_cast<const u32x4_t*>(slot + w_wave + b * 1024 + lane * 16);
+      if constexpr (FMT == kNF4)
+        sc[b] = *reinterpret_cast<const float*>(slot + s_wave + b * 256 + lane * 4);
+      else
+        sc[b] = e8m0_to_f32(*reinterpret_cast<const uint8_t*>(slot + s_wave + b * 256 + lane * 4));
+    }
+  };
+
+  // wf[rb][kk]: the weight operand of slice kk (rows of block rb).
+  u32x4_t wf[2][4];
+  // Two-phase decode of one slice of weights (a "target"): the lookup phase
+  // (NF4 pair-table reads) runs one slice ahead of the math phase (scale
+  // multiply, bf16 pack), so the table reads' latency hides behind a slice of
+  // MFMAs. Parity q alternates between targets.
+  float2 tp[2][2][4];   // NF4: table pairs [q][rb][byte of the dword]
+  unsigned traw[2][2];  // MXFP4: the packed dword [q][rb]
+  float ts[2][2];       // the target's scale [q][rb]
+  auto lookup = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2]) {
+    constexpr int q = decltype(QI)::value;
+    const unsigned x[2] = {x0, x1};
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      ts[q][b] = sc[b];
+      if constexpr (FMT == kNF4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const unsigned addr = __builtin_amdgcn_perm(x[b], reg2, 0x0C020000u | ((4u + i) << 8)) >> 1;
+          tp[q][b][i] = *reinterpret_cast<const float2*>(smem + addr);
+        }
+      } else {
+        traw[q][b] = x[b];
+      }
+    }
+  };
+  auto math = [&](auto QI, auto DI) {
+    constexpr int q = decltype(QI)::value;
+    constexpr int d = decltype(DI)::value;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      if constexpr (FMT == kNF4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          wf[b][d][i] = bf16x2_bits(tp[q][b][i].x * ts[q][b], tp[q][b][i].y * ts[q][b]);
+      } else {
+        wf[b][d] = mx_dword_to_bf16(traw[q][b], ts[q][b]);
+      }
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  // ---- pipeline. The loads of group g (activation stage of step g + 2,
+  // weights of step g + 3) start in slice 3 of step g - 1, right after the
+  // barrier that publishes step g's stage, and are spread over the next four
+  // slices (three per slice), so the barrier, the load issue and the operand
+  // reads of the next step's slice 0 all overlap MFMAs.
+  auto ao_of = [&](int g, int kk) { return a_off[kk] + uniform((g % 3) * kPtStage); };
+
+  // prologue: weights of step 0, groups -2 and -1
+  issue_w(0, 0, 4);
+  issue_a(0, 0, 8);
+  issue_w(1, 0, 4);
+  issue_a(1, 0, 8);
+  issue_w(2, 0, 4);
+  // step 0's stage and step 1's weights have landed for every wave, the
+  // pair table is complete
+  wait_vm_lgkm0<kPwGroupLoads>();
+  __builtin_amdgcn_s_barrier();
+  issue_a(2, 0, 3);   // the rest of this group goes out during step 0
+  u32x4_t wn[2];
+  float sn[2];
+  read_w(0, wn, sn);
+  lookup(I1{}, wn[0][0], wn[1][0], sn);
+  math(I1{}, I0{});
+  lookup(I1{}, wn[0][1], wn[1][1], sn);
+  math(I1{}, I1{});
+  lookup(I1{}, wn[0][2], wn[1][2], sn);
+  math(I1{}, I2{});
+  lookup(I0{}, wn[0][3], wn[1][3], sn);   // step 0's slice 3, decoded during its slice 0
+  read_w(1, wn, sn);
+  u32x4_t av[kM];
+#pragma unroll
+  for (int i = 0; i < kM; ++i)
+    av[i] = *reinterpret_cast<const u32x4_t*>(smem + ao_of(0, 0) + i * 4096);
+  f32x16_t acc[2][kM];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < kM; ++i) acc[b][i] = f32x16_t{};
+
+  // instruction mix of one slice, for the interleaving below
+  constexpr int kMf = 2 * kM;
+  constexpr int kValu = FMT == kNF4 ? 40 : 8;
+
+  for (int f = 0; f < F; ++f) {
+    int ao[4];
+#pragma unroll
+    for (int kk = 1; kk < 4; ++kk) ao[kk] = ao_of(f, kk);
+    ao[0] = ao_of(f + 1, 0);
+    // slice kk: its MFMAs, the next slice's operand reads, the lookup of the
+    // next target and the math of this slice's target (target of slice 0:
+    // this step's slice 3; of slices 1..3: the next step's slices 0..2).
+    // wn holds step f + 1's packed bytes.
+    auto slice = [&](auto KI) {
+      constexpr int kk = decltype(KI)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      // this slice's lookup input: for slice 3 it is saved before step
+      // f + 2's bytes replace wn
+      unsigned x0 = wn[0][kk], x1 = wn[1][kk];
+      float xs[2] = {sn[0], sn[1]};
+      if constexpr (kk == 3) {
+        // step f + 1's stage and step f + 2's weights have landed, every
+        // wave has read all of stage f: publish, and start refilling it
+        wait_vm_lgkm0<kPwGroupLoads>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        read_w(f + 2, wn, sn);
+      }
+      // this slice's share of the loads of group f + 1 (stage of step f + 3,
+      // weights of step f + 4; started in slice 3 of step f)
+      if constexpr (kk == 0) issue_a(f + 2, 3, 6);
+      if constexpr (kk == 1) { issue_a(f + 2, 6, 8); issue_w(f + 3, 0, 1); }
+      if constexpr (kk == 2) issue_w(f + 3, 1, 4);
+      if constexpr (kk == 3) issue_a(f + 3, 0, 3);
+#pragma unroll
+      for (int i = 0; i < kM; ++i) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          acc[b][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              as_bf16x8(wf[b][kk]), as_bf16x8(av[i]), acc[b][i], 0, 0, 0);
+        av[i] = *reinterpret_cast<const u32x4_t*>(smem + ao[(kk + 1) & 3] + i * 4096);
+      }
+      constexpr int qn = (kk + 1) & 1, qc = kk & 1;
+      lookup(std::integral_constant<int, qn>{}, x0, x1, xs);
+      math(std::integral_constant<int, qc>{}, std::integral_constant<int, (kk + 3) & 3>{});
+      // interleave: per MFMA, one LDS read, a few VALU instructions and (in
+      // slice 3) the next group's loads
+      constexpr int kDs = kM + (FMT == kNF4 ? 8 : 0) + (kk == 3 ? 3 : 0);
+      constexpr int kDsPer = (kDs + kMf - 1) / kMf;
+      constexpr int kValuPer = (kValu + kMf - 1) / kMf;
+      constexpr int kVmPer = 1;
+#pragma unroll
+      for (int j = 0; j < kMf; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
+        if constexpr (kVmPer > 0) __builtin_amdgcn_sched_group_barrier(0x020, kVmPer, 0);
+      }
+    };
+    slice(I0{});
+    slice(I1{});
+    slice(I2{});
+    slice(I3{});
+  }
+
+  // ---- epilogue: the bf16 tile goes through LDS (free now: every wave is
+  // past its last operand read), so the global stores write whole rows.
+  // LDS tile: row r at r * 512 bytes, 16-byte chunk c at (c ^ (r % 32)) * 16.
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vm_lgkm0<63>();
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int i = 0; i < kM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int row = i * 32 + l32;
+        const int col = wave * 64 + b * 32 + 8 * g + 4 * h;   // 4 columns
+        u32x2_t v;
+        v.x = bf16x2_bits(acc[b][i][4 * g + 0], acc[b][i][4 * g + 1]);
+        v.y = bf16x2_bits(acc[b][i][4 * g + 2], acc[b][i][4 * g + 3]);
+        *reinterpret_cast<u32x2_t*>(smem + row * 512 + (((col >> 3) ^ l32) << 4) + (col & 7) * 2) = v;
+      }
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      uniform_ptr(out + (int64_t)t.row0 * p.ldo), 0, uniform((int)((int64_t)t.rows * p.ldo * 2)),
+      0x00020000);
+  const int ldo2 = (int)(p.ldo * 2);
+  const int chunk = lane & 31;
+  const int col = t.n0 + chunk * 8;
+  const int coff = col < p.N ? col * 2 + h * ldo2 : kOOB;
+  // wave w stores rows 2 (4 j + w) + lane / 32, j = 0 .. 4 kM - 1
+#pragma unroll
+  for (int j = 0; j < kM * 4; ++j) {
+    const int row = (j * 4 + wave) * 2 + h;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * 512 + ((chunk ^ (row & 31)) << 4));
+    __builtin_amdgcn_raw_buffer_store_b128(v, ro, coff, uniform((j * 4 + wave) * 2 * ldo2), 0);
+  }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256, 1)
+    k_prefill_w(const FwdArgs p, const int32_t* __restrict__ t_row0,
+                const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
+                const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) char smem[kPwLds];
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);
+
+  // this workgroup's tile: XCD x = blockIdx % 8 takes the x-th contiguous
+  // eighth of the tile list, in dispatch order
+  const int n_tiles = (int)((p.N + kPfBN - 1) / kPfBN);
+  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
+  const int nx = gridDim.x >= 8 ? 8 : 1;
+  const int x = (int)(blockIdx.x % nx), idx = (int)(blockIdx.x / nx);
+  const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
+  const int64_t tg = lo + idx;
+  if (tg >= hi) return;
+  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
+  PfTile t;
+  const int mt = (int)(tg / n_tiles);
+  t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
+  t.row0 = t_row0[mt];
+  t.rows = t_rows[mt];
+  t.e = eids[t_group[mt]];
+  if (t.rows > 128)
+    prefill_w_tile<FMT, 8>(p, t, smem, out);
+  else if (t.rows > 64)
+    prefill_w_tile<FMT, 4>(p, t, smem, out);
+  else
+    prefill_w_tile<FMT, 2>(p, t, smem, out);
+}
+
+// ========================================================== tiled dgrad ==
+//
+// out[t, k] = sum_n grad[t, n] W[e][n, k]: the weights are read transposed.
+// Same skeleton as k_prefill -- 128-row tiles of one group x 256 output
+// columns (here: k), a persistent XCD-contiguous tile list, a 4-stage ring of
+// gradient rows filled by direct-to-LDS loads, one flat pipeline over (tile,
+// 64-wide n-step) -- with the weight operand going through LDS:
+//   * per step each thread loads 4 packed rows (n) x 8 columns (k) -- one
+//     dword per row -- decodes them and writes them transposed (k-major, 4
+//     consecutive n per 8-byte write) into a double-buffered bf16 tile of 256
+//     k-rows x 64 n, decoded during the step before the one that reads it;
+//   * wave w reads its 32 k-rows of that tile as MFMA operand A and the
+//     gradient rows from the stage as operand B (32 x 32 x 16 bf16).
+// The NF4 pair table here has 16 lane columns (32 KiB), so stages, weight
+// tiles and table fit the 160 KiB of LDS.
+constexpr int kDgTile = kPfBN;            // output columns (k) per tile
+constexpr int kDgStep = 64;               // n per step
+constexpr int kDgBStage = kDgTile * kDgStep * 2;
 
 template <int FMT>
 __global__ void __launch_bounds__(512, 2)
@@ -2083,6 +2443,15 @@ bool prefill_enabled() {
   return on;
 }
 
+// GNF4_PREFILL_W=0 keeps the eight-wave tall-tile kernel (k_prefill_t).
+bool prefill_w_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("GNF4_PREFILL_W");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <int FMT>
 int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
@@ -2097,6 +2466,14 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
     if (pf_ok && prefill_enabled() && block_m == kPtBM) {
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
       const int64_t grid = tiles < cus ? tiles : cus;
+      if (prefill_w_enabled() && (int64_t)kPtBM * p.ldo * 2 < 0x7FFFFFFF) {
+        // one tile per workgroup; the grid covers eight equal XCD ranges
+        const int64_t per_x = (tiles + 7) / 8;
+        if (per_x * 8 > 0x7FFFFFFF) return -1;
+        hipLaunchKernelGGL((k_prefill_w<FMT>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream, p,
+                           p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+        return hipGetLastError() == hipSuccess ? 0 : -2;
+      }
       hipLaunchKernelGGL((k_prefill_t<FMT>), dim3((unsigned)grid), dim3(512), 0, stream, p,
                          p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
       return hipGetLastError() == hipSuccess ? 0 : -2;

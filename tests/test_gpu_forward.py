@@ -344,3 +344,21 @@ def test_tall_tiles_give_the_bits_of_128_row_tiles(fmt, sizes):
     auto = op(a, W, S, sizes, ids)
     assert torch.equal(tall, short) and torch.equal(auto, tall)
     contract_check(fmt, tall, a, W, S, sizes, ids)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("N,K", [(320, 704), (2880, 2880), (96, 64)])
+def test_tall_tiles_ragged_weight_rows_and_step_counts(fmt, N, K):
+    """The four-wave tall-tile kernel with weight rows that do not fill its
+    256-row tile (N % 256 != 0), step counts that are not multiples of the
+    three-slot load rings (K / 64 = 11, 45, 1) and every row-subtile class
+    (<= 64, <= 128, > 128 rows): bitwise equal to 128-row tiles."""
+    sizes = [300, 40, 0, 100, 256, 129]
+    W, S = _stack(fmt, 6, N, K, seed=71)
+    ids = [5, 0, 3, 1, 2, 4]
+    a = rand_acts(sum(sizes), K, seed=72)
+    op = _ops()[fmt]
+    tall = op(a, W, S, sizes, ids, block_m=256)
+    short = op(a, W, S, sizes, ids, block_m=128)
+    assert torch.equal(tall, short)
+    contract_check(fmt, tall, a, W, S, sizes, ids)

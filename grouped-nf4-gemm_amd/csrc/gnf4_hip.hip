@@ -61,6 +61,7 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
 typedef __attribute__((ext_vector_type(2))) unsigned u32x2_t;
+typedef __attribute__((ext_vector_type(2))) int v2i32_t;
 
 constexpr int kNF4 = GNF4_FMT_NF4;
 constexpr int kMX = GNF4_FMT_MXFP4;
@@ -1520,13 +1521,32 @@ constexpr int kPwTab = 0x20000;                            // 16-column pair tab
 constexpr int kPwLds = kPwTab + 256 * 16 * 8;              // 160 KiB
 static_assert(kPwW0 + 3 * kPwWSlot <= kPwTab, "weight ring below the pair table");
 
-template <int FMT, int kM>
+// DG = true: the dgrad form, out[t, k] = sum_n grad[t, n] W[e][n, k]. The
+// grad rows stage like the forward's activations (the contraction runs over
+// n), t.n0 is the first output column k, and wave w owns the 64 columns
+// [t.n0 + 64 w, +64). Its weight operands come from the packed rows read
+// transposed: per step the wave's slot holds 64 rows (n) x 32 bytes (its 64
+// k), and one ds_read_b64_tr_b8 per slice hands each lane one byte column c
+// of the slice's 8 rows (lane half h: rows 32 h + 8 kk + 0..7, as the
+// forward's k mapping). Byte c holds k = 2c (high nibble) and 2c + 1 (low
+// nibble), which feed the two 32-column MFMA blocks b = 0 (even k) and
+// b = 1 (odd k), so block b, MFMA row i is column t.n0 + 64 w + 2 i + b.
+// The 16-byte rows of the tr8 read come in the order 0,2,4,6,1,3,5,7, so
+// dword 0 of the result holds the even rows and dword 1 the odd ones, and
+// the bf16 pairs (row 2m, row 2m + 1) come out of byte m of each. The
+// absmax of (row, the wave's 64-block) is staged per step as 64 floats.
+template <int FMT, int kM, bool DG>
 __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t, char* smem,
                                                uint16_t* __restrict__ out) {
+  static_assert(!DG || FMT == kNF4, "the transposed-read tile decodes NF4");
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
-  const int F = (int)((p.K + kPfBK - 1) / kPfBK);
+  // contraction length (forward: K; dgrad: N) and output width (N; K)
+  const int64_t Kc = DG ? p.N : p.K;
+  const int64_t Nout = DG ? p.K : p.N;
+  const int F = (int)((Kc + kPfBK - 1) / kPfBK);
+  constexpr int kGroupLoads = DG ? kPwAPieces + 3 : kPwGroupLoads;   // dgrad: 2 byte + 1 scale loads
   // table address << 1 | column * 16 (nf4_dword_to_bf16_t16)
   const unsigned reg2 = ((unsigned)kPwTab << 1) | (unsigned)(lane & 15) * 16u;
 
@@ -1553,12 +1573,23 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   const int b_bytes = (int)(p.N * p.sbn);
   const int s_bytes = (int)(p.N * p.ssn * kScaleBytes);
   int b_voff[2], s_voff[2];
+  if constexpr (DG) {
+    // step rows n0 + 32 rb + lane / 2, 16 bytes (lane % 2) of the wave's 32;
+    // per step only soffset (n0 rows) moves. A wave past K loads zeros.
+    const int64_t kw = t.n0 + wave * 64;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int64_t n = t.n0 + wave * 64 + rb * 32 + l32;
-    b_voff[rb] = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
-    if constexpr (FMT == kNF4) s_voff[rb] = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
-    else s_voff[rb] = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+    for (int rb = 0; rb < 2; ++rb)
+      b_voff[rb] = kw < p.K ? (int)((rb * 32 + (lane >> 1)) * p.sbn + kw / 2) + (lane & 1) * 16 : kOOB;
+    s_voff[0] = kw < p.K ? (int)(lane * p.ssn * 4 + (kw >> 6) * 4) : kOOB;
+    s_voff[1] = kOOB;
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int64_t n = t.n0 + wave * 64 + rb * 32 + l32;
+      b_voff[rb] = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
+      if constexpr (FMT == kNF4) s_voff[rb] = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
+      else s_voff[rb] = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+    }
   }
   // this wave's blocks of a weight slot: bytes (rb) at +rb KiB, lane-linear;
   // scales one dword per lane (direct-to-LDS loads of a byte still land in
@@ -1587,6 +1618,23 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   auto issue_w = [&](int g, int q0, int q1) {
     const bool live = g < F;
     const int k0 = live ? g * kPfBK : 0;
+    if constexpr (DG) {
+      // rows [k0, k0 + 64) of the contraction: 2 KiB of bytes, 64 scales
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+          uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
+      char* slot = smem + kPwW0 + uniform((g % 3) * kPwWSlot);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        if (b >= q0 && b < q1)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(slot + w_wave + b * 1024), 16,
+                                                   b_voff[b], uniform((int)(k0 * p.sbn)), 0, 0);
+      if (2 >= q0 && 2 < q1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave), 4, s_voff[0],
+                                                 uniform((int)(k0 * p.ssn * 4)), 0, 0);
+      return;
+    }
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1609,8 +1657,24 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     }
   };
   // this lane's packed bytes and scale of step g (block rb), from its slot
+  // dgrad: lane address of the tr8 read of slice kk (lane i of its 16-lane
+  // group supplies 8 bytes of row pi(i / 2), half i % 2 of the group's 16)
+  const int tr_off = w_wave + (32 * h + ((lane >> 1) & 3) * 2 + ((lane >> 3) & 1)) * 32 +
+                     ((lane >> 4) & 1) * 16 + (lane & 1) * 8;
   auto read_w = [&](int g, u32x4_t (&w)[2], float (&sc)[2]) {
     const char* slot = smem + kPwW0 + uniform((g % 3) * kPwWSlot);
+    if constexpr (DG) {
+      typedef __attribute__((address_space(3))) v2i32_t lds_v2i32;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const v2i32_t r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i32*)(lds_ptr_t)(slot + tr_off + kk * 8 * 32));
+        w[0][kk] = (unsigned)r.x;
+        w[1][kk] = (unsigned)r.y;
+      }
+      sc[0] = sc[1] = 0.f;
+      return;
+    }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       w[b] = *reinterpret_cast<const u32x4_t*>(slot + w_wave + b * 1024 + lane * 16);
@@ -1630,9 +1694,18 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   float2 tp[2][2][4];   // NF4: table pairs [q][rb][byte of the dword]
   unsigned traw[2][2];  // MXFP4: the packed dword [q][rb]
   float ts[2][2];       // the target's scale [q][rb]
-  auto lookup = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2]) {
+  float ts8[2][DG ? 8 : 1];   // dgrad: the scales of the target's 8 rows [q][row]
+  // (dgrad) g, kk: the target's step and slice, whose rows' scales it reads
+  auto lookup = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2], int g, int kk) {
     constexpr int q = decltype(QI)::value;
     const unsigned x[2] = {x0, x1};
+    if constexpr (DG) {
+      const char* sp = smem + kPwW0 + uniform((g % 3) * kPwWSlot) + s_wave + (32 * h + 8 * kk) * 4;
+      const float4 s0 = *reinterpret_cast<const float4*>(sp);
+      const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
+      ts8[q][0] = s0.x; ts8[q][1] = s0.y; ts8[q][2] = s0.z; ts8[q][3] = s0.w;
+      ts8[q][4] = s1.x; ts8[q][5] = s1.y; ts8[q][6] = s1.z; ts8[q][7] = s1.w;
+    }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       ts[q][b] = sc[b];
@@ -1650,6 +1723,15 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   auto math = [&](auto QI, auto DI) {
     constexpr int q = decltype(QI)::value;
     constexpr int d = decltype(DI)::value;
+    if constexpr (DG) {
+      // byte m of dword 0 / 1: rows 2m / 2m + 1; .x even k, .y odd k
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        wf[0][d][m] = bf16x2_bits(tp[q][0][m].x * ts8[q][2 * m], tp[q][1][m].x * ts8[q][2 * m + 1]);
+        wf[1][d][m] = bf16x2_bits(tp[q][0][m].y * ts8[q][2 * m], tp[q][1][m].y * ts8[q][2 * m + 1]);
+      }
+      return;
+    }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       if constexpr (FMT == kNF4) {
@@ -1681,19 +1763,19 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   issue_w(2, 0, 4);
   // step 0's stage and step 1's weights have landed for every wave, the
   // pair table is complete
-  wait_vm_lgkm0<kPwGroupLoads>();
+  wait_vm_lgkm0<kGroupLoads>();
   __builtin_amdgcn_s_barrier();
   issue_a(2, 0, 3);   // the rest of this group goes out during step 0
   u32x4_t wn[2];
   float sn[2];
   read_w(0, wn, sn);
-  lookup(I1{}, wn[0][0], wn[1][0], sn);
+  lookup(I1{}, wn[0][0], wn[1][0], sn, 0, 0);
   math(I1{}, I0{});
-  lookup(I1{}, wn[0][1], wn[1][1], sn);
+  lookup(I1{}, wn[0][1], wn[1][1], sn, 0, 1);
   math(I1{}, I1{});
-  lookup(I1{}, wn[0][2], wn[1][2], sn);
+  lookup(I1{}, wn[0][2], wn[1][2], sn, 0, 2);
   math(I1{}, I2{});
-  lookup(I0{}, wn[0][3], wn[1][3], sn);   // step 0's slice 3, decoded during its slice 0
+  lookup(I0{}, wn[0][3], wn[1][3], sn, 0, 3);   // step 0's slice 3, decoded during its slice 0
   read_w(1, wn, sn);
   u32x4_t av[kM];
 #pragma unroll
@@ -1728,7 +1810,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       if constexpr (kk == 3) {
         // step f + 1's stage and step f + 2's weights have landed, every
         // wave has read all of stage f: publish, and start refilling it
-        wait_vm_lgkm0<kPwGroupLoads>();
+        wait_vm_lgkm0<kGroupLoads>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         read_w(f + 2, wn, sn);
@@ -1748,11 +1830,11 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
         av[i] = *reinterpret_cast<const u32x4_t*>(smem + ao[(kk + 1) & 3] + i * 4096);
       }
       constexpr int qn = (kk + 1) & 1, qc = kk & 1;
-      lookup(std::integral_constant<int, qn>{}, x0, x1, xs);
+      lookup(std::integral_constant<int, qn>{}, x0, x1, xs, f + 1, kk);
       math(std::integral_constant<int, qc>{}, std::integral_constant<int, (kk + 3) & 3>{});
       // interleave: per MFMA, one LDS read, a few VALU instructions and (in
       // slice 3) the next group's loads
-      constexpr int kDs = kM + (FMT == kNF4 ? 8 : 0) + (kk == 3 ? 3 : 0);
+      constexpr int kDs = kM + (FMT == kNF4 ? 8 : 0) + (DG ? 2 : 0) + (kk == 3 ? 3 : 0);
       constexpr int kDsPer = (kDs + kMf - 1) / kMf;
       constexpr int kValuPer = (kValu + kMf - 1) / kMf;
       constexpr int kVmPer = 1;
@@ -1776,6 +1858,21 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   __builtin_amdgcn_sched_barrier(0);
   wait_vm_lgkm0<63>();
   __builtin_amdgcn_s_barrier();
+  if constexpr (DG) {
+    // MFMA row 8 g + 4 h + q of block b is column 64 w + 2 (8 g + 4 h + q) + b:
+    // the two blocks interleave into one 16-byte chunk 8 w + 2 g + h
+#pragma unroll
+    for (int i = 0; i < kM; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int row = i * 32 + l32;
+        const int chunk = wave * 8 + 2 * g + h;
+        u32x4_t v;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = bf16x2_bits(acc[0][i][4 * g + q], acc[1][i][4 * g + q]);
+        *reinterpret_cast<u32x4_t*>(smem + row * 512 + ((chunk ^ l32) << 4)) = v;
+      }
+  } else
 #pragma unroll
   for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -1797,7 +1894,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   const int ldo2 = (int)(p.ldo * 2);
   const int chunk = lane & 31;
   const int col = t.n0 + chunk * 8;
-  const int coff = col < p.N ? col * 2 + h * ldo2 : kOOB;
+  const int coff = col < Nout ? col * 2 + h * ldo2 : kOOB;
   // wave w stores rows 2 (4 j + w) + lane / 32, j = 0 .. 4 kM - 1
 #pragma unroll
   for (int j = 0; j < kM * 4; ++j) {
@@ -1807,7 +1904,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   }
 }
 
-template <int FMT>
+template <int FMT, bool DG = false>
 __global__ void __launch_bounds__(256, 1)
     k_prefill_w(const FwdArgs p, const int32_t* __restrict__ t_row0,
                 const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
@@ -1818,7 +1915,7 @@ __global__ void __launch_bounds__(256, 1)
 
   // this workgroup's tile: XCD x = blockIdx % 8 takes the x-th contiguous
   // eighth of the tile list, in dispatch order
-  const int n_tiles = (int)((p.N + kPfBN - 1) / kPfBN);
+  const int n_tiles = (int)(((DG ? p.K : p.N) + kPfBN - 1) / kPfBN);
   const int64_t total = (int64_t)p.n_mtiles * n_tiles;
   const int nx = gridDim.x >= 8 ? 8 : 1;
   const int x = (int)(blockIdx.x % nx), idx = (int)(blockIdx.x / nx);
@@ -1833,11 +1930,11 @@ __global__ void __launch_bounds__(256, 1)
   t.rows = t_rows[mt];
   t.e = eids[t_group[mt]];
   if (t.rows > 128)
-    prefill_w_tile<FMT, 8>(p, t, smem, out);
+    prefill_w_tile<FMT, 8, DG>(p, t, smem, out);
   else if (t.rows > 64)
-    prefill_w_tile<FMT, 4>(p, t, smem, out);
+    prefill_w_tile<FMT, 4, DG>(p, t, smem, out);
   else
-    prefill_w_tile<FMT, 2>(p, t, smem, out);
+    prefill_w_tile<FMT, 2, DG>(p, t, smem, out);
 }
 
 // ========================================================== tiled dgrad ==
@@ -2509,10 +2606,49 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+// GNF4_DGRAD_W=0 keeps NF4 dgrad on k_dgrad_tiled (at most 128-row tiles).
+bool dgrad_w_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("GNF4_DGRAD_W");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <int FMT>
 int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
+  if constexpr (FMT == kNF4) {
+    // the four-wave tile with transposed tr8 reads of the packed rows: any
+    // tile of at most 256 rows, whole 64-wide n steps and 64-wide k blocks
+    const bool w_ok = p.N % kDgStep == 0 && p.K % 64 == 0 && p.ldo % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPtBM &&
+                      (int64_t)kPtBM * p.ldg * 2 < 0x7FFFFFFF &&
+                      (int64_t)kPtBM * p.ldo * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF &&
+                      p.N * p.ssn * 4 < 0x7FFFFFFF;
+    if (w_ok && prefill_enabled() && dgrad_w_enabled()) {
+      FwdArgs f{};
+      f.a = p.g;
+      f.lda = p.ldg;
+      f.B = p.B;
+      f.sbe = p.sbe;
+      f.sbn = p.sbn;
+      f.S = p.S;
+      f.sse = p.sse;
+      f.ssn = p.ssn;
+      f.n_mtiles = p.n_mtiles;
+      f.N = p.N;
+      f.K = p.K;
+      f.ldo = p.ldo;
+      const int64_t tiles = (int64_t)p.n_mtiles * ((p.K + kPfBN - 1) / kPfBN);
+      const int64_t per_x = (tiles + 7) / 8;
+      if (per_x * 8 > 0x7FFFFFFF) return -1;
+      hipLaunchKernelGGL((k_prefill_w<FMT, true>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream,
+                         f, p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+      return hipGetLastError() == hipSuccess ? 0 : -2;
+    }
+  }
   const bool tiled_ok = p.N % kDgStep == 0 && p.ldo % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
                         (int64_t)kPfBM * p.ldg * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF;

@@ -557,8 +557,10 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     S = _scales_view(S)
     sizes_i = [int(m) for m in sizes]
     # tile height from the largest group, as in the forward (the kernel's
-    # per-row arithmetic does not depend on it)
-    bm = _kernel_block_m(_prefill_block_m(max(sizes_i)))
+    # per-row arithmetic does not depend on it); NF4 groups of more than 128
+    # rows take 256-row tiles (the four-wave transposed-read kernel)
+    bm = (_auto_block_m(max(sizes_i)) if fmt == _hiplib.FMT_NF4
+          else _kernel_block_m(_prefill_block_m(max(sizes_i))))
     t0, tr, tg = _tiles_host(sizes_i, bm)
     eids_dev = _eids_device(expert_ids, dev)
     if eids_dev is None:

@@ -122,3 +122,33 @@ def test_dgrad_qwen_down_shape_contract():
     e_f = rel_err(got, ref)
     e_d = rel_err(_oracle_bf16_path("nf4", go, W, S, sizes, ids), ref)
     assert e_f <= 1e-2 and e_f <= 2 * e_d, (e_f, e_d)
+
+
+def test_dgrad_nf4_tall_tiles_and_k_tails():
+    """Groups above 128 rows run 256-row tiles; K = 320 leaves one live
+    64-column block in the second 256-wide k tile."""
+    from nf4_grouped import dgrad_4bit_grouped
+    N, K = 192, 320
+    W, S = rand_nf4_stack(6, N, K, seed=12)
+    sizes, ids = [300, 129, 64, 1, 0, 200], [5, 0, 2, 3, 4, 1]
+    go = rand_acts(sum(sizes), N, seed=13)
+    got = dgrad_4bit_grouped(go, W, S, sizes, ids)
+    want = _oracle_bf16_path("nf4", go, W, S, sizes, ids)
+    assert rel_err(got, want) < 1e-2
+    ref = _fp64("nf4", go, W, S, sizes, ids)
+    e_f, e_d = rel_err(got, ref), rel_err(want, ref)
+    assert e_f <= 1e-2 and e_f <= 2 * e_d, (e_f, e_d)
+
+
+def test_dgrad_nf4_tall_one_hot_rows_are_exact():
+    """Every row of a 300-row group one-hot at n = t % N reproduces decoded
+    row t % N bit for bit, through both 256-row tiles."""
+    from nf4_grouped import dgrad_4bit_grouped
+    N, K, T = 128, 320, 300
+    W, S = rand_nf4_stack(2, N, K, seed=14)
+    go = torch.zeros(T, N, dtype=torch.bfloat16, device="cuda")
+    t = torch.arange(T, device="cuda")
+    go[t, t % N] = 1
+    got = dgrad_4bit_grouped(go, W, S, [T], [1])
+    dec = dequant("nf4", W[1], S[1]).to(torch.bfloat16)
+    assert torch.equal(got, dec[(t % N)])

@@ -1511,6 +1511,16 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // LDS map: activation stages at 0, 32 and 64 KiB; weight ring at 96 KiB
 // (three 10 KiB slots: 8 KiB of packed bytes, then the scales); the 16-column
 // NF4 pair table at 128 KiB.
+#ifdef GNF4_TRACE
+// timestamp trace (probe builds only): per workgroup 8 words
+__device__ unsigned long long g_pw_trace[65536 * 8];
+#define PW_TRACE(slot) do { if (threadIdx.x == 0) { g_pw_trace[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memtime(); } } while (0)
+#else
+#define PW_TRACE(slot) do { } while (0)
+#endif
+#ifndef GNF4_ABL
+#define GNF4_ABL 0   // ablation builds only: 1 no decode, 2 no MFMA, 4 no step barrier, 8/16 no loads
+#endif
 constexpr int kPwWaves = 4;
 constexpr int kPwRowsPerWave = kPtBM / kPwWaves;           // 64 activation rows staged per wave
 constexpr int kPwAPieces = kPtStage / 1024 / kPwWaves;     // 8 direct-to-LDS loads per wave
@@ -1537,7 +1547,7 @@ static_assert(kPwW0 + 3 * kPwWSlot <= kPwTab, "weight ring below the pair table"
 // absmax of (row, the wave's 64-block) is staged per step as 64 floats.
 template <int FMT, int kM, bool DG>
 __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t, char* smem,
-                                               uint16_t* __restrict__ out) {
+                                               uint16_t* __restrict__ out, const int lut) {
   static_assert(!DG || FMT == kNF4, "the transposed-read tile decodes NF4");
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -1604,6 +1614,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // activation pieces [p0, p1) of step g, and weight loads [q0, q1) of step g
   // (0, 1: packed bytes of row blocks 0, 1; 2, 3: their scales).
   auto issue_a = [&](int g, int p0, int p1) {
+    if constexpr (GNF4_ABL & 8) { if (g > 2) return; }
     const bool live = g < F;
     const int k0 = live ? g * kPfBK : 0;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
@@ -1616,6 +1627,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
                                                  uniform(k0 * 2), 0, 0);
   };
   auto issue_w = [&](int g, int q0, int q1) {
+    if constexpr (GNF4_ABL & 16) { if (g > 2) return; }
     const bool live = g < F;
     const int k0 = live ? g * kPfBK : 0;
     if constexpr (DG) {
@@ -1687,6 +1699,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
 
   // wf[rb][kk]: the weight operand of slice kk (rows of block rb).
   u32x4_t wf[2][4];
+  const unsigned x_abl = (unsigned)lane * 0x00010001u;   // ablation builds only
   // Two-phase decode of one slice of weights (a "target"): the lookup phase
   // (NF4 pair-table reads) runs one slice ahead of the math phase (scale
   // multiply, bf16 pack), so the table reads' latency hides behind a slice of
@@ -1695,53 +1708,65 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   unsigned traw[2][2];  // MXFP4: the packed dword [q][rb]
   float ts[2][2];       // the target's scale [q][rb]
   float ts8[2][DG ? 8 : 1];   // dgrad: the scales of the target's 8 rows [q][row]
+  // Both phases come in 8 pieces (pc), so the slice loop can spread them
+  // over its MFMA pairs.
+  // Lookup piece pc: NF4 table pair of byte pc % 4 of dword pc / 4 (dgrad:
+  // piece 0 also reads the target rows' 8 scales); MXFP4 keeps dword pc.
   // (dgrad) g, kk: the target's step and slice, whose rows' scales it reads
-  auto lookup = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2], int g, int kk) {
+  auto lookup_pc = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2], int g, int kk,
+                       int pc) {
     constexpr int q = decltype(QI)::value;
-    const unsigned x[2] = {x0, x1};
+    if constexpr (GNF4_ABL & 1) return;
+    const int b = pc >> 2, i = pc & 3;
+    const unsigned xb = b ? x1 : x0;
     if constexpr (DG) {
-      const char* sp = smem + kPwW0 + uniform((g % 3) * kPwWSlot) + s_wave + (32 * h + 8 * kk) * 4;
-      const float4 s0 = *reinterpret_cast<const float4*>(sp);
-      const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
-      ts8[q][0] = s0.x; ts8[q][1] = s0.y; ts8[q][2] = s0.z; ts8[q][3] = s0.w;
-      ts8[q][4] = s1.x; ts8[q][5] = s1.y; ts8[q][6] = s1.z; ts8[q][7] = s1.w;
+      if (pc == 0) {
+        const char* sp = smem + kPwW0 + uniform((g % 3) * kPwWSlot) + s_wave + (32 * h + 8 * kk) * 4;
+        const float4 s0 = *reinterpret_cast<const float4*>(sp);
+        const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
+        ts8[q][0] = s0.x; ts8[q][1] = s0.y; ts8[q][2] = s0.z; ts8[q][3] = s0.w;
+        ts8[q][4] = s1.x; ts8[q][5] = s1.y; ts8[q][6] = s1.z; ts8[q][7] = s1.w;
+      }
     }
-#pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      ts[q][b] = sc[b];
-      if constexpr (FMT == kNF4) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const unsigned addr = __builtin_amdgcn_perm(x[b], reg2, 0x0C020000u | ((4u + i) << 8)) >> 1;
-          tp[q][b][i] = *reinterpret_cast<const float2*>(smem + addr);
-        }
-      } else {
-        traw[q][b] = x[b];
+    if constexpr (FMT == kNF4) {
+      if (i == 0) ts[q][b] = sc[b];
+      unsigned addr = __builtin_amdgcn_perm(xb, reg2, 0x0C020000u | ((4u + i) << 8)) >> 1;
+      if constexpr (GNF4_ABL & 64) addr = uniform(addr);
+      tp[q][b][i] = *reinterpret_cast<const float2*>(smem + addr);
+    } else {
+      if (pc < 2) {
+        traw[q][pc] = pc ? x1 : x0;
+        ts[q][pc] = sc[pc];
       }
     }
   };
-  auto math = [&](auto QI, auto DI) {
+  // Math piece pc: one bf16-pair dword of operand block pc / 4, dword pc % 4
+  // (dgrad: dword pc / 2 of block pc % 2); MXFP4 converts block pc whole.
+  auto math_pc = [&](auto QI, auto DI, int pc) {
     constexpr int q = decltype(QI)::value;
     constexpr int d = decltype(DI)::value;
+    if constexpr (GNF4_ABL & 1) { wf[pc >> 2][d][pc & 3] = x_abl ^ pc; return; }
     if constexpr (DG) {
       // byte m of dword 0 / 1: rows 2m / 2m + 1; .x even k, .y odd k
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        wf[0][d][m] = bf16x2_bits(tp[q][0][m].x * ts8[q][2 * m], tp[q][1][m].x * ts8[q][2 * m + 1]);
+      const int m = pc >> 1;
+      if (pc & 1)
         wf[1][d][m] = bf16x2_bits(tp[q][0][m].y * ts8[q][2 * m], tp[q][1][m].y * ts8[q][2 * m + 1]);
-      }
-      return;
+      else
+        wf[0][d][m] = bf16x2_bits(tp[q][0][m].x * ts8[q][2 * m], tp[q][1][m].x * ts8[q][2 * m + 1]);
+    } else if constexpr (FMT == kNF4) {
+      const int b = pc >> 2, i = pc & 3;
+      wf[b][d][i] = bf16x2_bits(tp[q][b][i].x * ts[q][b], tp[q][b][i].y * ts[q][b]);
+    } else {
+      if (pc < 2) wf[pc][d] = mx_dword_to_bf16(traw[q][pc], ts[q][pc]);
     }
+  };
+  auto lookup = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2], int g, int kk) {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      if constexpr (FMT == kNF4) {
+    for (int pc = 0; pc < 8; ++pc) lookup_pc(QI, x0, x1, sc, g, kk, pc);
+  };
+  auto math = [&](auto QI, auto DI) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          wf[b][d][i] = bf16x2_bits(tp[q][b][i].x * ts[q][b], tp[q][b][i].y * ts[q][b]);
-      } else {
-        wf[b][d] = mx_dword_to_bf16(traw[q][b], ts[q][b]);
-      }
-    }
+    for (int pc = 0; pc < 8; ++pc) math_pc(QI, DI, pc);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -1755,16 +1780,20 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // reads of the next step's slice 0 all overlap MFMAs.
   auto ao_of = [&](int g, int kk) { return a_off[kk] + uniform((g % 3) * kPtStage); };
 
+  PW_TRACE(1);
   // prologue: weights of step 0, groups -2 and -1
   issue_w(0, 0, 4);
   issue_a(0, 0, 8);
   issue_w(1, 0, 4);
   issue_a(1, 0, 8);
   issue_w(2, 0, 4);
+  // the NF4 pair table is built while the first loads are in flight
+  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
   // step 0's stage and step 1's weights have landed for every wave, the
   // pair table is complete
   wait_vm_lgkm0<kGroupLoads>();
   __builtin_amdgcn_s_barrier();
+  PW_TRACE(2);
   issue_a(2, 0, 3);   // the rest of this group goes out during step 0
   u32x4_t wn[2];
   float sn[2];
@@ -1810,40 +1839,54 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       if constexpr (kk == 3) {
         // step f + 1's stage and step f + 2's weights have landed, every
         // wave has read all of stage f: publish, and start refilling it
+        if constexpr (!(GNF4_ABL & 4)) {
         wait_vm_lgkm0<kGroupLoads>();
         __builtin_amdgcn_s_barrier();
+        }
         __builtin_amdgcn_sched_barrier(0);
         read_w(f + 2, wn, sn);
       }
-      // this slice's share of the loads of group f + 1 (stage of step f + 3,
-      // weights of step f + 4; started in slice 3 of step f)
-      if constexpr (kk == 0) issue_a(f + 2, 3, 6);
-      if constexpr (kk == 1) { issue_a(f + 2, 6, 8); issue_w(f + 3, 0, 1); }
-      if constexpr (kk == 2) issue_w(f + 3, 1, 4);
-      if constexpr (kk == 3) issue_a(f + 3, 0, 3);
+      constexpr int qn = (kk + 1) & 1, qc = kk & 1;
+      using QN = std::integral_constant<int, qn>;
+      using QC = std::integral_constant<int, qc>;
+      using DT = std::integral_constant<int, (kk + 3) & 3>;
+      constexpr int kPer = 8 / kM;
+      // per 32-row subtile i: its two MFMAs, the reload of its operand for
+      // the next slice, and 8 / kM pieces of the lookup (next target) and of
+      // the math (this slice's target), fenced so that the decode work sits
+      // between MFMAs and runs while they execute
 #pragma unroll
       for (int i = 0; i < kM; ++i) {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
+          if constexpr (!(GNF4_ABL & 2))
           acc[b][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               as_bf16x8(wf[b][kk]), as_bf16x8(av[i]), acc[b][i], 0, 0, 0);
+        if constexpr (!(GNF4_ABL & 32))
         av[i] = *reinterpret_cast<const u32x4_t*>(smem + ao[(kk + 1) & 3] + i * 4096);
-      }
-      constexpr int qn = (kk + 1) & 1, qc = kk & 1;
-      lookup(std::integral_constant<int, qn>{}, x0, x1, xs, f + 1, kk);
-      math(std::integral_constant<int, qc>{}, std::integral_constant<int, (kk + 3) & 3>{});
-      // interleave: per MFMA, one LDS read, a few VALU instructions and (in
-      // slice 3) the next group's loads
-      constexpr int kDs = kM + (FMT == kNF4 ? 8 : 0) + (DG ? 2 : 0) + (kk == 3 ? 3 : 0);
-      constexpr int kDsPer = (kDs + kMf - 1) / kMf;
-      constexpr int kValuPer = (kValu + kMf - 1) / kMf;
-      constexpr int kVmPer = 1;
+        else av[i][0] ^= (unsigned)kk;
+        if constexpr (GNF4_ABL & 2) { acc[0][i][0] += __builtin_bit_cast(float, av[i][0]); }
+        // this slice's share of the loads of group f + 1 (stage of step
+        // f + 3, weights of step f + 4; started in slice 3 of step f): three
+        // loads, spread over the subtiles so the vector-memory queue never
+        // takes a burst
 #pragma unroll
-      for (int j = 0; j < kMf; ++j) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, kDsPer, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, kValuPer, 0);
-        if constexpr (kVmPer > 0) __builtin_amdgcn_sched_group_barrier(0x020, kVmPer, 0);
+        for (int j = 0; j < 3; ++j) {
+          if ((j * kM) / 3 != i) continue;
+          if constexpr (kk == 0) issue_a(f + 2, 3 + j, 4 + j);
+          if constexpr (kk == 1) {
+            if (j < 2) issue_a(f + 2, 6 + j, 7 + j);
+            else issue_w(f + 3, 0, 1);
+          }
+          if constexpr (kk == 2) issue_w(f + 3, 1 + j, 2 + j);
+          if constexpr (kk == 3) issue_a(f + 3, j, j + 1);
+        }
+#pragma unroll
+        for (int pc = i * kPer; pc < (i + 1) * kPer; ++pc) {
+          lookup_pc(QN{}, x0, x1, xs, f + 1, kk, pc);
+          math_pc(QC{}, DT{}, pc);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
     slice(I0{});
@@ -1852,6 +1895,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     slice(I3{});
   }
 
+  PW_TRACE(3);
   // ---- epilogue: the bf16 tile goes through LDS (free now: every wave is
   // past its last operand read), so the global stores write whole rows.
   // LDS tile: row r at r * 512 bytes, 16-byte chunk c at (c ^ (r % 32)) * 16.
@@ -1902,6 +1946,17 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * 512 + ((chunk ^ (row & 31)) << 4));
     __builtin_amdgcn_raw_buffer_store_b128(v, ro, coff, uniform((j * 4 + wave) * 2 * ldo2), 0);
   }
+  PW_TRACE(4);
+#ifdef GNF4_TRACE
+  if (threadIdx.x == 0) {
+    unsigned hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    g_pw_trace[blockIdx.x * 8 + 5] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
+    g_pw_trace[blockIdx.x * 8 + 7] = __builtin_amdgcn_s_memrealtime();
+  }
+#endif
 }
 
 template <int FMT, bool DG = false>
@@ -1922,7 +1977,10 @@ __global__ void __launch_bounds__(256, 1)
   const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
   const int64_t tg = lo + idx;
   if (tg >= hi) return;
-  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
+  PW_TRACE(0);
+#ifdef GNF4_TRACE
+  if (threadIdx.x == 0) g_pw_trace[blockIdx.x * 8 + 6] = __builtin_amdgcn_s_memrealtime();
+#endif
   PfTile t;
   const int mt = (int)(tg / n_tiles);
   t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
@@ -1930,11 +1988,11 @@ __global__ void __launch_bounds__(256, 1)
   t.rows = t_rows[mt];
   t.e = eids[t_group[mt]];
   if (t.rows > 128)
-    prefill_w_tile<FMT, 8, DG>(p, t, smem, out);
+    prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut);
   else if (t.rows > 64)
-    prefill_w_tile<FMT, 4, DG>(p, t, smem, out);
+    prefill_w_tile<FMT, 4, DG>(p, t, smem, out, lut);
   else
-    prefill_w_tile<FMT, 2, DG>(p, t, smem, out);
+    prefill_w_tile<FMT, 2, DG>(p, t, smem, out, lut);
 }
 
 // ========================================================== tiled dgrad ==
@@ -2748,6 +2806,11 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 extern "C" {
 
 int gnf4_hip_abi_version(void) { return GNF4_HIP_ABI_VERSION; }
+#ifdef GNF4_TRACE
+int gnf4_trace_dump(void* host, int n) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pw_trace), (size_t)n * 8) == hipSuccess ? 0 : -1;
+}
+#endif
 
 int gnf4_hip_device_cus(void) { return device_cus(); }
 

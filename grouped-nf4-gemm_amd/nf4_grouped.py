@@ -257,6 +257,34 @@ def _tiles_host(sizes, block_m: int):
     return t_row0, t_rows, t_group
 
 
+# relative cost of a 256-row tile by height class (<= 64, <= 128, > 128 rows):
+# the four-wave kernel skips the MFMAs of empty 32-row subtiles, but every
+# tile decodes its whole weight slice
+_TALL_TILE_COST = (0.45, 0.62, 1.0)
+
+
+def _xcd_balanced(t_row0, t_rows, t_group):
+    """Order 256-row tiles for the four-wave kernels, which hand XCD x the
+    x-th contiguous eighth of the tile list: tiles go, by decreasing cost,
+    to the least loaded of 8 bins of exactly those sizes, and each bin runs
+    its tiles largest first, same-expert tiles adjacent. Only the
+    order changes; every output row is computed the same way."""
+    n = len(t_row0)
+    if n < 16:
+        return t_row0, t_rows, t_group
+    cost = [_TALL_TILE_COST[2 if r > 128 else (1 if r > 64 else 0)] for r in t_rows]
+    key = lambda i: (-cost[i], t_group[i], t_row0[i])
+    cap = [n * (x + 1) // 8 - n * x // 8 for x in range(8)]   # the kernel's ranges
+    bins, load = [[] for _ in range(8)], [0.0] * 8
+    for i in sorted(range(n), key=key):
+        x = min((x for x in range(8) if len(bins[x]) < cap[x]), key=lambda x: (load[x], x))
+        bins[x].append(i)
+        load[x] += cost[i]
+    order = [i for b in bins for i in sorted(b, key=key)]
+    return ([t_row0[i] for i in order], [t_rows[i] for i in order],
+            [t_group[i] for i in order])
+
+
 def build_group_tiles(sizes, block_m: int, device):
     """Expand jagged group sizes into fixed M-tiles: ``(row0, valid_rows,
     group_idx)`` int32 device tensors, one transfer for all three
@@ -453,6 +481,8 @@ class GroupPlan:
             self.block_m = (_kernel_block_m(block_m) if block_m is not None
                             else _auto_block_m(self.max_m))
             t0, tr, tg = _tiles_host(sizes_i, self.block_m)
+            if self.block_m == 256:
+                t0, tr, tg = _xcd_balanced(t0, tr, tg)
             self.eids = torch.tensor(ids, dtype=torch.int32, device=dev)
             self.row_off = None
             self.tables = tuple(torch.tensor(v, dtype=torch.int32, device=dev) for v in (t0, tr, tg))
@@ -526,6 +556,8 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     else:
         bm = _kernel_block_m(block_m) if block_m is not None else _auto_block_m(max_m)
         t0, tr, tg = _tiles_host(sizes_i, bm)
+        if bm == 256:
+            t0, tr, tg = _xcd_balanced(t0, tr, tg)
         e_h, t0_d, tr_d, tg_d = to_device_i32((host_eids, t0, tr, tg), dev)
         eids = eids_dev if eids_dev is not None else e_h
         args = (eids.data_ptr(), None, G, t0_d.data_ptr(), tr_d.data_ptr(),
@@ -562,6 +594,8 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     bm = (_auto_block_m(max(sizes_i)) if fmt == _hiplib.FMT_NF4
           else _kernel_block_m(_prefill_block_m(max(sizes_i))))
     t0, tr, tg = _tiles_host(sizes_i, bm)
+    if bm == 256:
+        t0, tr, tg = _xcd_balanced(t0, tr, tg)
     eids_dev = _eids_device(expert_ids, dev)
     if eids_dev is None:
         _check_host_ids(expert_ids, E)

@@ -257,30 +257,22 @@ def _tiles_host(sizes, block_m: int):
     return t_row0, t_rows, t_group
 
 
-# relative cost of a 256-row tile by height class (<= 64, <= 128, > 128 rows):
-# the four-wave kernel skips the MFMAs of empty 32-row subtiles, but every
-# tile decodes its whole weight slice
-_TALL_TILE_COST = (0.45, 0.62, 1.0)
-
-
 def _xcd_balanced(t_row0, t_rows, t_group):
     """Order 256-row tiles for the four-wave kernels, which hand XCD x the
-    x-th contiguous eighth of the tile list: tiles go, by decreasing cost,
-    to the least loaded of 8 bins of exactly those sizes, and each bin runs
-    its tiles largest first, same-expert tiles adjacent. Only the
-    order changes; every output row is computed the same way."""
+    x-th contiguous eighth of the tile list: the tiles, largest height class
+    first (group order within a class), are dealt round robin to 8 bins,
+    which then run back to back. Each bin gets an equal share of every
+    class and runs its largest tiles first. Only the order changes; every
+    output row is computed the same way. O(n), no sort: the input is in group
+    order already."""
     n = len(t_row0)
     if n < 16:
         return t_row0, t_rows, t_group
-    cost = [_TALL_TILE_COST[2 if r > 128 else (1 if r > 64 else 0)] for r in t_rows]
-    key = lambda i: (-cost[i], t_group[i], t_row0[i])
-    cap = [n * (x + 1) // 8 - n * x // 8 for x in range(8)]   # the kernel's ranges
-    bins, load = [[] for _ in range(8)], [0.0] * 8
-    for i in sorted(range(n), key=key):
-        x = min((x for x in range(8) if len(bins[x]) < cap[x]), key=lambda x: (load[x], x))
-        bins[x].append(i)
-        load[x] += cost[i]
-    order = [i for b in bins for i in sorted(b, key=key)]
+    by_class = ([], [], [])
+    for i, r in enumerate(t_rows):
+        by_class[2 if r > 128 else (1 if r > 64 else 0)].append(i)
+    ranked = by_class[2] + by_class[1] + by_class[0]
+    order = [i for x in range(8) for i in ranked[x::8]]
     return ([t_row0[i] for i in order], [t_rows[i] for i in order],
             [t_group[i] for i in order])
 

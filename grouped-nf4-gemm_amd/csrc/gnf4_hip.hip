@@ -1511,20 +1511,9 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // LDS map: activation stages at 0, 32 and 64 KiB; weight ring at 96 KiB
 // (three 10 KiB slots: 8 KiB of packed bytes, then the scales); the 16-column
 // NF4 pair table at 128 KiB.
-#ifdef GNF4_TRACE
-// timestamp trace (probe builds only): per workgroup 8 words
-__device__ unsigned long long g_pw_trace[65536 * 8];
-#define PW_TRACE(slot) do { if (threadIdx.x == 0) { g_pw_trace[blockIdx.x * 8 + (slot)] = __builtin_amdgcn_s_memtime(); } } while (0)
-#else
-#define PW_TRACE(slot) do { } while (0)
-#endif
-#ifndef GNF4_ABL
-#define GNF4_ABL 0   // ablation builds only: 1 no decode, 2 no MFMA, 4 no step barrier, 8/16 no loads
-#endif
 constexpr int kPwWaves = 4;
 constexpr int kPwRowsPerWave = kPtBM / kPwWaves;           // 64 activation rows staged per wave
 constexpr int kPwAPieces = kPtStage / 1024 / kPwWaves;     // 8 direct-to-LDS loads per wave
-constexpr int kPwGroupLoads = kPwAPieces + 4;              // + 2 weight + 2 scale loads
 constexpr int kPwW0 = 3 * kPtStage;                        // weight ring
 constexpr int kPwWSlot = 10 * 1024;                     // 8 KiB packed bytes + 4 waves x 2 x 256 B scales
 constexpr int kPwTab = 0x20000;                            // 16-column pair table
@@ -1556,7 +1545,9 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   const int64_t Kc = DG ? p.N : p.K;
   const int64_t Nout = DG ? p.K : p.N;
   const int F = (int)((Kc + kPfBK - 1) / kPfBK);
-  constexpr int kGroupLoads = DG ? kPwAPieces + 3 : kPwGroupLoads;   // dgrad: 2 byte + 1 scale loads
+  // per step: activation pieces, 2 weight-byte loads, scale loads (NF4: one
+  // of 64 rows; MXFP4: two of 32 rows x 2 blocks)
+  constexpr int kGroupLoads = kPwAPieces + 2 + (FMT == kNF4 ? 1 : 2);
   // table address << 1 | column * 16 (nf4_dword_to_bf16_t16)
   const unsigned reg2 = ((unsigned)kPwTab << 1) | (unsigned)(lane & 15) * 16u;
 
@@ -1593,12 +1584,19 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     s_voff[0] = kw < p.K ? (int)(lane * p.ssn * 4 + (kw >> 6) * 4) : kOOB;
     s_voff[1] = kOOB;
   } else {
+    // loading lane i: row 32 rb + i / 2 of the wave's 64, 16-byte half i % 2
+    // (two lanes per row keep each lane quad on two cache lines); NF4
+    // scales: row i, one load; MXFP4 scales: row 32 rb + i / 2, block i % 2
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int64_t n = t.n0 + wave * 64 + rb * 32 + l32;
-      b_voff[rb] = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
-      if constexpr (FMT == kNF4) s_voff[rb] = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
-      else s_voff[rb] = n < p.N ? (int)(n * p.ssn) + h : kOOB;
+      const int64_t n = t.n0 + wave * 64 + rb * 32 + (lane >> 1);
+      b_voff[rb] = n < p.N ? (int)(n * p.sbn) + (lane & 1) * 16 : kOOB;
+      if constexpr (FMT != kNF4) s_voff[rb] = n < p.N ? (int)(n * p.ssn) + (lane & 1) : kOOB;
+    }
+    if constexpr (FMT == kNF4) {
+      const int64_t n = t.n0 + wave * 64 + lane;
+      s_voff[0] = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
+      s_voff[1] = kOOB;
     }
   }
   // this wave's blocks of a weight slot: bytes (rb) at +rb KiB, lane-linear;
@@ -1614,7 +1612,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // activation pieces [p0, p1) of step g, and weight loads [q0, q1) of step g
   // (0, 1: packed bytes of row blocks 0, 1; 2, 3: their scales).
   auto issue_a = [&](int g, int p0, int p1) {
-    if constexpr (GNF4_ABL & 8) { if (g > 2) return; }
     const bool live = g < F;
     const int k0 = live ? g * kPfBK : 0;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
@@ -1627,7 +1624,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
                                                  uniform(k0 * 2), 0, 0);
   };
   auto issue_w = [&](int g, int q0, int q1) {
-    if constexpr (GNF4_ABL & 16) { if (g > 2) return; }
     const bool live = g < F;
     const int k0 = live ? g * kPfBK : 0;
     if constexpr (DG) {
@@ -1657,15 +1653,17 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       if (b >= q0 && b < q1)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(slot + w_wave + b * 1024), 16,
                                                  b_voff[b], uniform(k0 >> 1), 0, 0);
+    if constexpr (FMT == kNF4) {
+      if (2 >= q0 && 2 < q1)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave), 4, s_voff[0],
+                                                 uniform((k0 >> 6) * 4), 0, 0);
+    } else {
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-      if (b + 2 < q0 || b + 2 >= q1) continue;
-      if constexpr (FMT == kNF4)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave + b * 256), 4,
-                                                 s_voff[b], uniform((k0 >> 6) * 4), 0, 0);
-      else
+      for (int b = 0; b < 2; ++b) {
+        if (b + 2 < q0 || b + 2 >= q1) continue;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave + b * 256), 1,
                                                  s_voff[b], uniform(k0 >> 5), 0, 0);
+      }
     }
   };
   // this lane's packed bytes and scale of step g (block rb), from its slot
@@ -1689,17 +1687,17 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      w[b] = *reinterpret_cast<const u32x4_t*>(slot + w_wave + b * 1024 + lane * 16);
+      w[b] = *reinterpret_cast<const u32x4_t*>(slot + w_wave + b * 1024 + (2 * l32 + h) * 16);
       if constexpr (FMT == kNF4)
-        sc[b] = *reinterpret_cast<const float*>(slot + s_wave + b * 256 + lane * 4);
+        sc[b] = *reinterpret_cast<const float*>(slot + s_wave + (b * 32 + l32) * 4);
       else
-        sc[b] = e8m0_to_f32(*reinterpret_cast<const uint8_t*>(slot + s_wave + b * 256 + lane * 4));
+        sc[b] = e8m0_to_f32(
+            *reinterpret_cast<const uint8_t*>(slot + s_wave + b * 256 + (2 * l32 + h) * 4));
     }
   };
 
   // wf[rb][kk]: the weight operand of slice kk (rows of block rb).
   u32x4_t wf[2][4];
-  const unsigned x_abl = (unsigned)lane * 0x00010001u;   // ablation builds only
   // Two-phase decode of one slice of weights (a "target"): the lookup phase
   // (NF4 pair-table reads) runs one slice ahead of the math phase (scale
   // multiply, bf16 pack), so the table reads' latency hides behind a slice of
@@ -1716,7 +1714,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   auto lookup_pc = [&](auto QI, unsigned x0, unsigned x1, const float (&sc)[2], int g, int kk,
                        int pc) {
     constexpr int q = decltype(QI)::value;
-    if constexpr (GNF4_ABL & 1) return;
     const int b = pc >> 2, i = pc & 3;
     const unsigned xb = b ? x1 : x0;
     if constexpr (DG) {
@@ -1731,7 +1728,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     if constexpr (FMT == kNF4) {
       if (i == 0) ts[q][b] = sc[b];
       unsigned addr = __builtin_amdgcn_perm(xb, reg2, 0x0C020000u | ((4u + i) << 8)) >> 1;
-      if constexpr (GNF4_ABL & 64) addr = uniform(addr);
       tp[q][b][i] = *reinterpret_cast<const float2*>(smem + addr);
     } else {
       if (pc < 2) {
@@ -1745,7 +1741,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   auto math_pc = [&](auto QI, auto DI, int pc) {
     constexpr int q = decltype(QI)::value;
     constexpr int d = decltype(DI)::value;
-    if constexpr (GNF4_ABL & 1) { wf[pc >> 2][d][pc & 3] = x_abl ^ pc; return; }
     if constexpr (DG) {
       // byte m of dword 0 / 1: rows 2m / 2m + 1; .x even k, .y odd k
       const int m = pc >> 1;
@@ -1780,7 +1775,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // reads of the next step's slice 0 all overlap MFMAs.
   auto ao_of = [&](int g, int kk) { return a_off[kk] + uniform((g % 3) * kPtStage); };
 
-  PW_TRACE(1);
   // prologue: weights of step 0, groups -2 and -1
   issue_w(0, 0, 4);
   issue_a(0, 0, 8);
@@ -1793,7 +1787,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // pair table is complete
   wait_vm_lgkm0<kGroupLoads>();
   __builtin_amdgcn_s_barrier();
-  PW_TRACE(2);
   issue_a(2, 0, 3);   // the rest of this group goes out during step 0
   u32x4_t wn[2];
   float sn[2];
@@ -1839,10 +1832,8 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       if constexpr (kk == 3) {
         // step f + 1's stage and step f + 2's weights have landed, every
         // wave has read all of stage f: publish, and start refilling it
-        if constexpr (!(GNF4_ABL & 4)) {
         wait_vm_lgkm0<kGroupLoads>();
         __builtin_amdgcn_s_barrier();
-        }
         __builtin_amdgcn_sched_barrier(0);
         read_w(f + 2, wn, sn);
       }
@@ -1859,13 +1850,9 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       for (int i = 0; i < kM; ++i) {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
-          if constexpr (!(GNF4_ABL & 2))
           acc[b][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               as_bf16x8(wf[b][kk]), as_bf16x8(av[i]), acc[b][i], 0, 0, 0);
-        if constexpr (!(GNF4_ABL & 32))
         av[i] = *reinterpret_cast<const u32x4_t*>(smem + ao[(kk + 1) & 3] + i * 4096);
-        else av[i][0] ^= (unsigned)kk;
-        if constexpr (GNF4_ABL & 2) { acc[0][i][0] += __builtin_bit_cast(float, av[i][0]); }
         // this slice's share of the loads of group f + 1 (stage of step
         // f + 3, weights of step f + 4; started in slice 3 of step f): three
         // loads, spread over the subtiles so the vector-memory queue never
@@ -1895,7 +1882,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     slice(I3{});
   }
 
-  PW_TRACE(3);
   // ---- epilogue: the bf16 tile goes through LDS (free now: every wave is
   // past its last operand read), so the global stores write whole rows.
   // LDS tile: row r at r * 512 bytes, 16-byte chunk c at (c ^ (r % 32)) * 16.
@@ -1946,17 +1932,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * 512 + ((chunk ^ (row & 31)) << 4));
     __builtin_amdgcn_raw_buffer_store_b128(v, ro, coff, uniform((j * 4 + wave) * 2 * ldo2), 0);
   }
-  PW_TRACE(4);
-#ifdef GNF4_TRACE
-  if (threadIdx.x == 0) {
-    unsigned hw;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-    unsigned xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    g_pw_trace[blockIdx.x * 8 + 5] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
-    g_pw_trace[blockIdx.x * 8 + 7] = __builtin_amdgcn_s_memrealtime();
-  }
-#endif
 }
 
 template <int FMT, bool DG = false>
@@ -1977,10 +1952,6 @@ __global__ void __launch_bounds__(256, 1)
   const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
   const int64_t tg = lo + idx;
   if (tg >= hi) return;
-  PW_TRACE(0);
-#ifdef GNF4_TRACE
-  if (threadIdx.x == 0) g_pw_trace[blockIdx.x * 8 + 6] = __builtin_amdgcn_s_memrealtime();
-#endif
   PfTile t;
   const int mt = (int)(tg / n_tiles);
   t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
@@ -2806,11 +2777,6 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 extern "C" {
 
 int gnf4_hip_abi_version(void) { return GNF4_HIP_ABI_VERSION; }
-#ifdef GNF4_TRACE
-int gnf4_trace_dump(void* host, int n) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pw_trace), (size_t)n * 8) == hipSuccess ? 0 : -1;
-}
-#endif
 
 int gnf4_hip_device_cus(void) { return device_cus(); }
 

@@ -1534,10 +1534,11 @@ static_assert(kPwW0 + 3 * kPwWSlot <= kPwTab, "weight ring below the pair table"
 // dword 0 of the result holds the even rows and dword 1 the odd ones, and
 // the bf16 pairs (row 2m, row 2m + 1) come out of byte m of each. The
 // absmax of (row, the wave's 64-block) is staged per step as 64 floats.
+// MXFP4 (low nibble = even k) converts each row's byte with that row's e8m0
+// scale of the lane's 32-column block and pairs rows with a byte permute.
 template <int FMT, int kM, bool DG>
 __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t, char* smem,
                                                uint16_t* __restrict__ out, const int lut) {
-  static_assert(!DG || FMT == kNF4, "the transposed-read tile decodes NF4");
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
@@ -1581,8 +1582,15 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
       b_voff[rb] = kw < p.K ? (int)((rb * 32 + (lane >> 1)) * p.sbn + kw / 2) + (lane & 1) * 16 : kOOB;
-    s_voff[0] = kw < p.K ? (int)(lane * p.ssn * 4 + (kw >> 6) * 4) : kOOB;
-    s_voff[1] = kOOB;
+    if constexpr (FMT == kNF4) {
+      s_voff[0] = kw < p.K ? (int)(lane * p.ssn * 4 + (kw >> 6) * 4) : kOOB;
+      s_voff[1] = kOOB;
+    } else {
+      // two e8m0 blocks (32 k each) per row: load bl stages block bl of 64 rows
+#pragma unroll
+      for (int bl = 0; bl < 2; ++bl)
+        s_voff[bl] = kw < p.K ? (int)(lane * p.ssn + (kw >> 5) + bl) : kOOB;
+    }
   } else {
     // loading lane i: row 32 rb + i / 2 of the wave's 64, 16-byte half i % 2
     // (two lanes per row keep each lane quad on two cache lines); NF4
@@ -1638,9 +1646,17 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
         if (b >= q0 && b < q1)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(slot + w_wave + b * 1024), 16,
                                                    b_voff[b], uniform((int)(k0 * p.sbn)), 0, 0);
-      if (2 >= q0 && 2 < q1)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave), 4, s_voff[0],
-                                                 uniform((int)(k0 * p.ssn * 4)), 0, 0);
+      if constexpr (FMT == kNF4) {
+        if (2 >= q0 && 2 < q1)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave), 4, s_voff[0],
+                                                   uniform((int)(k0 * p.ssn * 4)), 0, 0);
+      } else {
+#pragma unroll
+        for (int bl = 0; bl < 2; ++bl)
+          if (bl + 2 >= q0 && bl + 2 < q1)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(slot + s_wave + bl * 256), 1,
+                                                     s_voff[bl], uniform((int)(k0 * p.ssn)), 0, 0);
+      }
       return;
     }
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
@@ -1718,11 +1734,26 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     const unsigned xb = b ? x1 : x0;
     if constexpr (DG) {
       if (pc == 0) {
-        const char* sp = smem + kPwW0 + uniform((g % 3) * kPwWSlot) + s_wave + (32 * h + 8 * kk) * 4;
-        const float4 s0 = *reinterpret_cast<const float4*>(sp);
-        const float4 s1 = *reinterpret_cast<const float4*>(sp + 16);
-        ts8[q][0] = s0.x; ts8[q][1] = s0.y; ts8[q][2] = s0.z; ts8[q][3] = s0.w;
-        ts8[q][4] = s1.x; ts8[q][5] = s1.y; ts8[q][6] = s1.z; ts8[q][7] = s1.w;
+        // MXFP4: the lane's byte column c = lane % 32 holds k = 2c, 2c + 1,
+        // in scale block c / 16; each staged byte sits in its own dword
+        const char* sp = smem + kPwW0 + uniform((g % 3) * kPwWSlot) + s_wave + (32 * h + 8 * kk) * 4 +
+                         (FMT == kNF4 ? 0 : (l32 >> 4) * 256);
+        const u32x4_t s0 = *reinterpret_cast<const u32x4_t*>(sp);
+        const u32x4_t s1 = *reinterpret_cast<const u32x4_t*>(sp + 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if constexpr (FMT == kNF4) {
+            ts8[q][r] = __uint_as_float(s0[r]);
+            ts8[q][4 + r] = __uint_as_float(s1[r]);
+          } else {
+            ts8[q][r] = e8m0_to_f32(s0[r] & 0xFFu);
+            ts8[q][4 + r] = e8m0_to_f32(s1[r] & 0xFFu);
+          }
+        }
+      }
+      if constexpr (FMT != kNF4) {
+        if (pc < 2) traw[q][pc] = pc ? x1 : x0;
+        return;
       }
     }
     if constexpr (FMT == kNF4) {
@@ -1741,7 +1772,24 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   auto math_pc = [&](auto QI, auto DI, int pc) {
     constexpr int q = decltype(QI)::value;
     constexpr int d = decltype(DI)::value;
-    if constexpr (DG) {
+    if constexpr (DG && FMT != kNF4) {
+      // byte m of dword 0 / 1: rows 2m / 2m + 1, low nibble even k; the
+      // convert applies each row's own scale, a byte permute pairs the rows
+      if (pc & 1) return;
+      const int m = pc >> 1;
+      auto cvt = [&](unsigned x, float sc) {
+        bf16x2_t v;
+        if (m == 0) v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 0);
+        else if (m == 1) v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 1);
+        else if (m == 2) v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 2);
+        else v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 3);
+        return __builtin_bit_cast(unsigned, v);
+      };
+      const unsigned c0 = cvt(traw[q][0], ts8[q][2 * m]);
+      const unsigned c1 = cvt(traw[q][1], ts8[q][2 * m + 1]);
+      wf[0][d][m] = __builtin_amdgcn_perm(c1, c0, 0x05040100u);
+      wf[1][d][m] = __builtin_amdgcn_perm(c1, c0, 0x07060302u);
+    } else if constexpr (DG) {
       // byte m of dword 0 / 1: rows 2m / 2m + 1; .x even k, .y odd k
       const int m = pc >> 1;
       if (pc & 1)
@@ -1810,8 +1858,6 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
     for (int i = 0; i < kM; ++i) acc[b][i] = f32x16_t{};
 
   // instruction mix of one slice, for the interleaving below
-  constexpr int kMf = 2 * kM;
-  constexpr int kValu = FMT == kNF4 ? 40 : 8;
 
   for (int f = 0; f < F; ++f) {
     int ao[4];
@@ -2635,7 +2681,7 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-// GNF4_DGRAD_W=0 keeps NF4 dgrad on k_dgrad_tiled (at most 128-row tiles).
+// GNF4_DGRAD_W=0 keeps dgrad on k_dgrad_tiled (at most 128-row tiles).
 bool dgrad_w_enabled() {
   static const bool on = [] {
     const char* v = getenv("GNF4_DGRAD_W");
@@ -2648,7 +2694,7 @@ template <int FMT>
 int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
-  if constexpr (FMT == kNF4) {
+  {
     // the four-wave tile with transposed tr8 reads of the packed rows: any
     // tile of at most 256 rows, whole 64-wide n steps and 64-wide k blocks
     const bool w_ok = p.N % kDgStep == 0 && p.K % 64 == 0 && p.ldo % 4 == 0 &&

@@ -566,6 +566,19 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     return out
 
 
+def _dgrad_block_m(max_rows: int, N: int, K: int) -> int:
+    """Tile height of a dgrad launch: 256-row tiles when the four-wave
+    transposed-read kernel takes the shape (whole 64-wide n steps and k
+    blocks), else the forward's group-size rule capped at 128 rows (the
+    eight-wave dgrad kernels). ``GNF4_DGRAD_W=0`` or ``GNF4_PREFILL=0`` in
+    the environment (read by the library too) keep the eight-wave kernels."""
+    four_wave = (os.environ.get("GNF4_DGRAD_W", "1")[:1] != "0"
+                 and os.environ.get("GNF4_PREFILL", "1")[:1] != "0")
+    if max_rows > 128 and four_wave and N % 64 == 0 and K % 64 == 0:
+        return 256
+    return _kernel_block_m(_prefill_block_m(max_rows))
+
+
 def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     lib = _hiplib.load()
     E, N, half = W.shape
@@ -583,8 +596,7 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     # tile height from the largest group, as in the forward (the kernel's
     # per-row arithmetic does not depend on it); NF4 groups of more than 128
     # rows take 256-row tiles (the four-wave transposed-read kernel)
-    bm = (_auto_block_m(max(sizes_i)) if fmt == _hiplib.FMT_NF4
-          else _kernel_block_m(_prefill_block_m(max(sizes_i))))
+    bm = _dgrad_block_m(max(sizes_i), N, K)
     t0, tr, tg = _tiles_host(sizes_i, bm)
     if bm == 256:
         t0, tr, tg = _xcd_balanced(t0, tr, tg)

@@ -124,31 +124,54 @@ def test_dgrad_qwen_down_shape_contract():
     assert e_f <= 1e-2 and e_f <= 2 * e_d, (e_f, e_d)
 
 
-def test_dgrad_nf4_tall_tiles_and_k_tails():
-    """Groups above 128 rows run 256-row tiles; K = 320 leaves one live
-    64-column block in the second 256-wide k tile."""
-    from nf4_grouped import dgrad_4bit_grouped
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_dgrad_tall_tiles_and_k_tails(fmt):
+    """Groups above 128 rows run 256-row tiles (the four-wave transposed-read
+    kernel); K = 320 leaves one live 64-column block in the second 256-wide
+    k tile."""
     N, K = 192, 320
-    W, S = rand_nf4_stack(6, N, K, seed=12)
+    W, S = _stack(fmt, 6, N, K, seed=12)
     sizes, ids = [300, 129, 64, 1, 0, 200], [5, 0, 2, 3, 4, 1]
     go = rand_acts(sum(sizes), N, seed=13)
-    got = dgrad_4bit_grouped(go, W, S, sizes, ids)
-    want = _oracle_bf16_path("nf4", go, W, S, sizes, ids)
+    got = _ops()[fmt](go, W, S, sizes, ids)
+    want = _oracle_bf16_path(fmt, go, W, S, sizes, ids)
     assert rel_err(got, want) < 1e-2
-    ref = _fp64("nf4", go, W, S, sizes, ids)
+    ref = _fp64(fmt, go, W, S, sizes, ids)
     e_f, e_d = rel_err(got, ref), rel_err(want, ref)
     assert e_f <= 1e-2 and e_f <= 2 * e_d, (e_f, e_d)
 
 
-def test_dgrad_nf4_tall_one_hot_rows_are_exact():
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_dgrad_tall_one_hot_rows_are_exact(fmt):
     """Every row of a 300-row group one-hot at n = t % N reproduces decoded
     row t % N bit for bit, through both 256-row tiles."""
-    from nf4_grouped import dgrad_4bit_grouped
     N, K, T = 128, 320, 300
-    W, S = rand_nf4_stack(2, N, K, seed=14)
+    W, S = _stack(fmt, 2, N, K, seed=14)
     go = torch.zeros(T, N, dtype=torch.bfloat16, device="cuda")
     t = torch.arange(T, device="cuda")
     go[t, t % N] = 1
-    got = dgrad_4bit_grouped(go, W, S, [T], [1])
-    dec = dequant("nf4", W[1], S[1]).to(torch.bfloat16)
+    got = _ops()[fmt](go, W, S, [T], [1])
+    dec = dequant(fmt, W[1], S[1]).to(torch.bfloat16)
     assert torch.equal(got, dec[(t % N)])
+
+
+def test_dgrad_tall_mxfp4_scale_extremes():
+    """Small and large e8m0 exponents through the transposed-read kernel: each
+    row of a block has its own scale, and one-hot rows give the decoded
+    weights exactly. e8m0 0x00 (2^-127, subnormal results) may come out
+    flushed to zero, as in the forward's e8m0 edge test."""
+    N, K, T = 64, 128, 200
+    W, S = rand_mx_stack(1, N, K, seed=15)
+    S = S.clone()
+    S[0, 1::5, 1] = 2
+    S[0, 2::7, 3] = 140
+    S[0, ::3, 0] = 0
+    go = torch.zeros(T, N, dtype=torch.bfloat16, device="cuda")
+    t = torch.arange(T, device="cuda")
+    go[t, t % N] = 1
+    got = _ops()["mxfp4"](go, W, S, [T], [0])
+    want = dequant("mxfp4", W[0], S[0]).to(torch.bfloat16)[t % N]
+    sub = torch.zeros_like(want, dtype=torch.bool)
+    sub[:, :32] = (S[0, :, 0] == 0)[t % N].unsqueeze(1)
+    assert torch.equal(got[~sub], want[~sub])
+    assert bool(((got[sub] == want[sub]) | (got[sub] == 0)).all())

@@ -31,9 +31,10 @@
  *                    [n_mtiles] int32 (reference build_group_tiles,
  *                    kernel/nf4_grouped.py:334-362) with block_m in
  *                    {16, 32, 64, 128, 256}; t_rows[i] <= block_m. 256
- *                    (forward only) selects the tall MFMA kernel and needs
+ *                    selects the four-wave tall-tile kernel and needs
  *                    K % 64 == 0, N % 4 == 0, ldo % 4 == 0 and an 8-byte
- *                    aligned out (-1 otherwise).
+ *                    aligned out (-1 otherwise). The tile order is free
+ *                    (each XCD takes a contiguous eighth of the list).
  *
  * Return codes (the reference CPU tier's convention, gnf4_native/cpu_kernels.c:745-761):
  *   0 success, -1 shape or argument violation, -2 launch error.
@@ -156,7 +157,9 @@ int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t 
  * contracting over N in fixed 64-wide ascending steps (output bits do not
  * depend on block_m). grad_out is [T, ldg] bf16, out is [T, ldo] bf16 with
  * ldo >= K. Tile table as for the forward tiled path (n_mtiles may be 0:
- * nothing to do). */
+ * nothing to do). With N % 64 == 0 and K % 64 == 0 any block_m up to 256
+ * runs the four-wave transposed-read kernel; other shapes need
+ * block_m <= 128 (-1 otherwise). */
 int gnf4_hip_grouped_dgrad(int fmt, const void *grad_out, int g_dtype, int64_t ldg,
                            const uint8_t *B, int64_t stride_be, int64_t stride_bn,
                            const void *scales, int64_t stride_se, int64_t stride_sn,

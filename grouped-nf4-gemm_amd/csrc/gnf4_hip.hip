@@ -1826,11 +1826,16 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // prologue: weights of step 0, groups -2 and -1
   issue_w(0, 0, 4);
   issue_a(0, 0, 8);
+  // the NF4 pair table is built while the first loads are in flight
+  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
+  // step 0's weight bytes and scales have landed (the activation pieces may
+  // not have): their cache lines also hold the next steps' bytes and scales
+  // of the same rows, so steps 1 and 2 hit in L2 instead of queueing a second
+  // and third miss per row behind the first
+  wait_vm_lgkm0<kPwAPieces>();
   issue_w(1, 0, 4);
   issue_a(1, 0, 8);
   issue_w(2, 0, 4);
-  // the NF4 pair table is built while the first loads are in flight
-  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
   // step 0's stage and step 1's weights have landed for every wave, the
   // pair table is complete
   wait_vm_lgkm0<kGroupLoads>();

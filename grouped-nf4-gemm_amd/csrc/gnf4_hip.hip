@@ -332,8 +332,8 @@ __device__ __forceinline__ float bf16_round(float f) {
 // loads are issued and before any activation load (kFfnDn).
 template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces, int kKind,
           class Wait>
-__device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, char* smem,
-                                            const int lut, const int64_t ffn_h,
+__device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const int64_t nu,
+                                            char* smem, const int lut, const int64_t ffn_h,
                                             const int64_t ffn_n_dn, uint32_t* ffn_sync,
                                             const Wait& wait_acts) {
   // kFfnDn reads h, written by other workgroups during this launch, with
@@ -348,16 +348,30 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, c
   const int nl = lane & 15;
   const int q = lane >> 4;
   const unsigned lane_off = (unsigned)(lane & 31) * 8u;
-  const int64_t n_units =
-      kKind == kFfnGu ? ffn_h / 16 : (p.N + 16 * kTiles - 1) / (16 * kTiles);
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
 
-  const int g = (int)(u / n_units);
-  const int64_t nu = u - (int64_t)g * n_units;
-  const int r0 = p.row_off ? p.row_off[g] : g;
-  const int M = p.row_off ? p.row_off[g + 1] - r0 : 1;
+  // the expert id and the group's rows in one round trip of scalar loads
+  // (their latency heads every weight load): a null row_off reads the id
+  // twice instead of branching
+  const int32_t* ce = p.eids + g;
+  const int32_t* cr = p.row_off ? p.row_off + g : ce;
+  const int32_t* cr1 = p.row_off ? cr + 1 : ce;
+  const int one = p.row_off ? 1 : 0;
+  int e32, ro_a, ro_b;
+  // (written out: the compiler otherwise waits for the id before it sends
+  // the row-offset loads)
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(ce), "s"(cr), "s"(cr1)
+      : "memory");
+  const int64_t e = e32;
+  const int r0 = one ? ro_a : g;
+  const int M = one ? ro_b - ro_a : 1;
   if (M <= 0) return;  // uniform across the workgroup (empty group)
-  const int64_t e = p.eids[g];
   const int K32 = (int)p.K;
   const int kslices = K32 >> 3;                       // 16-byte activation pieces per row
   const int a_base = FMT == kNF4 ? 8 * kPairEntries : 0;
@@ -570,12 +584,22 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int64_t u, c
 // Decode path: one unit per workgroup.
 template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces>
 // two workgroups per CU: kDecodeWaves / 2 waves per SIMD
+// The grid is (units per group, G): the unit is read off the block
+// coordinates, with no division (G <= 65535 on this path).
 __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_fwd(const FwdArgs p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
   __builtin_amdgcn_sched_barrier(0);  // the codebook load goes out first
+  // every argument the unit needs, fetched in one round trip before the
+  // expert id (left to itself the compiler fetches them in several rounds,
+  // each behind a branch)
+  const FwdArgs q = p;
+  asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ldo));
+  const int g = (int)blockIdx.y;   // < G: the grid has exactly G rows of units
   decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain>(
-      p, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, NoWait{});
+      q, g, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, NoWait{});
 }
 
 // ------------------------------------------------------------ fused FFN --
@@ -619,12 +643,14 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
   const int64_t gu_units = (int64_t)gu.G * gu_per_group;
   const int64_t u = blockIdx.x;
   if (u < gu_units) {
-    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, u, smem, lut, H, dn.N, sync,
-                                                     NoWait{});
+    // unit counts stay below 2^31 (the launch checks): 32-bit division
+    const int gg = (int)((uint32_t)u / (uint32_t)gu_per_group);
+    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, gg, u - (int64_t)gg * gu_per_group, smem,
+                                                     lut, H, dn.N, sync, NoWait{});
     return;
   }
   const int64_t d = u - gu_units;
-  const int g = (int)(d / dn_per_group);
+  const int g = (int)((uint32_t)d / (uint32_t)dn_per_group);
   const int M = dn.row_off ? dn.row_off[g + 1] - dn.row_off[g] : 1;
   if (M <= 0) return;                   // empty group: no gate/up unit sets its flags
   uint32_t* row = sync + kFfnFlagBase + d * gu_per_group;
@@ -652,7 +678,8 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, d, smem, lut, 0, 0, sync, wait_h);
+  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, g, d - (int64_t)g * dn_per_group, smem, lut,
+                                                   0, 0, sync, wait_h);
 }
 
 // Elementwise silu-multiply for the unfused path (and groups too large for
@@ -2491,7 +2518,7 @@ int64_t clamp_grid(int64_t work, int64_t cap) { return work < cap ? (work > 0 ? 
 
 // Launch one decode-kernel instance with `lds` bytes of dynamic LDS.
 template <int FMT, int CPW, int T, int W, int PA>
-int launch_decode_inst(const FwdArgs& p, int64_t grid, int lds, hipStream_t stream) {
+int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream) {
   static int configured_dev = -1;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -2;
@@ -2501,13 +2528,12 @@ int launch_decode_inst(const FwdArgs& p, int64_t grid, int lds, hipStream_t stre
       return -2;
     configured_dev = dev;
   }
-  hipLaunchKernelGGL((k_decode_fwd<FMT, CPW, T, W, PA>), dim3((unsigned)grid), dim3(64 * W),
-                     lds, stream, p);
+  hipLaunchKernelGGL((k_decode_fwd<FMT, CPW, T, W, PA>), grid, dim3(64 * W), lds, stream, p);
   return 0;
 }
 
 template <int FMT, int CPW, int T>
-int launch_decode_pa(const FwdArgs& p, int64_t grid, int pa, int lds, hipStream_t stream) {
+int launch_decode_pa(const FwdArgs& p, dim3 grid, int pa, int lds, hipStream_t stream) {
   constexpr int W = 8;
   switch (pa) {
     case 1: return launch_decode_inst<FMT, CPW, T, W, 1>(p, grid, lds, stream);
@@ -2525,8 +2551,11 @@ template <int FMT, int kT>
 int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   constexpr int kW = 8;
   const int64_t per_wave = ((p.K + 127) / 128 + kW - 1) / kW;
-  const int64_t grid = (int64_t)p.G * ((p.N + 16 * kT - 1) / (16 * kT));
-  if (grid > 0x7FFFFFFF) return -1;
+  const int64_t n_units = (p.N + 16 * kT - 1) / (16 * kT);
+  if (p.G <= 0 || n_units == 0) return 0;
+  if ((int64_t)p.G * n_units > 0x7FFFFFFF || n_units > 0x7FFFFFFF) return -1;
+  if (p.G > 65535) return -1;   // grid rows (launch_decode splits larger calls)
+  const dim3 grid((unsigned)n_units, (unsigned)p.G, 1);
   // LDS staging covers at most 4 pieces of 16 bytes per thread
   const bool stage = p.max_m <= 2 && (int64_t)p.max_m * p.K * 2 <= 4 * 64 * kW * 16;
   const int64_t a_bytes = stage ? (int64_t)p.max_m * p.K * 2 : 0;
@@ -2550,10 +2579,25 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
 
 // Unit height: 32 rows, or 16 for single-row MXFP4 groups (more workgroups
 // for a stream that needs little decode work per byte).
+// Groups go to the grid's rows, at most 65535 per launch: larger calls run as
+// several launches over consecutive group ranges.
 template <int FMT>
 int launch_decode(const FwdArgs& p, hipStream_t stream) {
-  if (FMT == kMX && p.max_m == 1) return launch_decode_t<FMT, 1>(p, stream);
-  return launch_decode_t<FMT, 2>(p, stream);
+  for (int g0 = 0; g0 < p.G; g0 += 65535) {
+    FwdArgs q = p;
+    q.G = p.G - g0 < 65535 ? p.G - g0 : 65535;
+    q.eids = p.eids + g0;
+    if (p.row_off) {
+      q.row_off = p.row_off + g0;   // absolute row offsets
+    } else {                        // group g is row g
+      q.a = p.a + (int64_t)g0 * p.lda;
+      q.out = p.out + (int64_t)g0 * p.ldo;
+    }
+    const int rc = FMT == kMX && p.max_m == 1 ? launch_decode_t<FMT, 1>(q, stream)
+                                              : launch_decode_t<FMT, 2>(q, stream);
+    if (rc) return rc;
+  }
+  return 0;
 }
 
 // Fused FFN decode launch (every group at most 16 rows). Phase shapes:

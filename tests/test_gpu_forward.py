@@ -362,3 +362,21 @@ def test_tall_tiles_ragged_weight_rows_and_step_counts(fmt, N, K):
     short = op(a, W, S, sizes, ids, block_m=128)
     assert torch.equal(tall, short)
     contract_check(fmt, tall, a, W, S, sizes, ids)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_decode_more_than_65535_one_row_groups(fmt):
+    """One-row groups beyond the grid's 65535 rows run as several launches
+    over consecutive group ranges: every row equals the same row computed in
+    a smaller call, bit for bit, and the whole meets the contract."""
+    E, N, K, T = 4, 32, 128, 70000
+    W, S = _stack(fmt, E, N, K, seed=21)
+    a = rand_acts(T, K, seed=22)
+    ids = torch.randint(0, E, (T,), generator=torch.Generator().manual_seed(23)).tolist()
+    op = _ops()[fmt]
+    out = op(a, W, S, [1] * T, ids)
+    head = op(a[:40000], W, S, [1] * 40000, ids[:40000])
+    tail = op(a[40000:], W, S, [1] * (T - 40000), ids[40000:])
+    assert torch.equal(out, torch.cat([head, tail]))
+    sel = list(range(0, T, 997))
+    contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel), [ids[i] for i in sel])

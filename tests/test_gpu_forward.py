@@ -380,3 +380,34 @@ def test_decode_more_than_65535_one_row_groups(fmt):
     assert torch.equal(out, torch.cat([head, tail]))
     sel = list(range(0, T, 997))
     contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel), [ids[i] for i in sel])
+
+
+@pytest.mark.parametrize("fmt,N,K", [("nf4", 1536, 2048), ("nf4", 2048, 768), ("mxfp4", 2880, 2880),
+                                     ("mxfp4", 640, 1440)])
+def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
+    """A group's decoded rows are the same bits in a launch of many units as
+    in a launch of that group alone, and the whole meets the contract.
+    Covers ragged groups, empty groups, a K tail (2880 = 22.5 chunks) and N
+    past a 128-row boundary."""
+    E = 24
+    W, S = _stack(fmt, E, N, K, seed=31)
+    g = torch.Generator().manual_seed(32)
+    G = 120 if N >= 1536 else 400
+    sizes = torch.randint(0, 17, (G,), generator=g).tolist()
+    sizes[3] = 0
+    sizes[5] = 16
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    a = rand_acts(sum(sizes), K, seed=33)
+    op = _ops()[fmt]
+    out = op(a, W, S, sizes, ids)
+    row = 0
+    for gi in (0, 1, 5, G - 1):
+        r0 = sum(sizes[:gi])
+        m = sizes[gi]
+        if m == 0:
+            continue
+        alone = op(a[r0:r0 + m], W, S, [m], [ids[gi]])
+        assert torch.equal(out[r0:r0 + m], alone), f"group {gi} differs"
+    sel = list(range(0, sum(sizes), 7))
+    contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel),
+                   [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])

@@ -264,8 +264,9 @@ def ffn_report(model):
     return r
 
 
-def time_graph(fn, steps, warmup, dev):
-    """Capture fn() as a graph, then time `steps` replays after `warmup`."""
+def time_graph(fn, steps, warmup, dev, settle=False):
+    """Capture fn() as a graph, then time `steps` replays after `warmup`
+    (and, with `settle`, after further replays filling 30 ms)."""
     import torch
     fn()
     torch.cuda.synchronize()
@@ -282,6 +283,13 @@ def time_graph(fn, steps, warmup, dev):
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
+    # settle: replay until 30 ms of GPU work has run since the last idle
+    # stretch, so the shader clock has left its idle level (a heavy kernel
+    # right after idle runs ~10 % slower for a few milliseconds)
+    t_w = time.perf_counter()
+    while settle and time.perf_counter() - t_w < 0.03:
+        graph.replay()
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         graph.replay()
@@ -337,7 +345,7 @@ def _timed(fn, dev, reps=10):
     captured launches and group-table copies without the host-side planning,
     the eager figure is what a Python caller sees per op call."""
     import torch
-    ms_graph, _ = time_graph(fn, reps, 3, dev)
+    ms_graph, _ = time_graph(fn, reps, 3, dev, settle=True)
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     evs[0].record()

@@ -24,6 +24,8 @@ dequant-then-matmul path against an fp64 reference, and <= 1e-2.
 from __future__ import annotations
 
 import os
+
+import numpy as np
 import threading
 
 import torch
@@ -179,7 +181,8 @@ class _PinnedRing:
                 buf = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
                 self.slots[i] = buf
             host = buf[:n]
-            host.copy_(torch.tensor(flat, dtype=torch.int32))
+            host.copy_(torch.from_numpy(flat) if isinstance(flat, np.ndarray)
+                       else torch.tensor(flat, dtype=torch.int32))
             out = host.to(dev, non_blocking=True)
             if ev is None:
                 ev = torch.cuda.Event()
@@ -217,16 +220,21 @@ def to_device_i32(seqs, device):
     dev = torch.device(device)
     if total == 0:
         return [torch.empty(0, dtype=torch.int32, device=dev) for _ in seqs]
-    flat = [int(v) for s in seqs for v in (s.tolist() if torch.is_tensor(s) else s)]
+    if all(isinstance(s, np.ndarray) for s in seqs):   # the launch paths' tile tables
+        flat = np.concatenate([s.astype(np.int32, copy=False) for s in seqs])
+    else:
+        flat = [int(v) for s in seqs for v in (s.tolist() if torch.is_tensor(s) else s)]
     cuda = dev.type == "cuda" and torch.cuda.is_available()
     if not cuda:
-        packed = torch.tensor(flat, dtype=torch.int32, device=dev)
+        packed = (torch.from_numpy(flat).to(dev) if isinstance(flat, np.ndarray)
+                  else torch.tensor(flat, dtype=torch.int32, device=dev))
     else:
         ar = _arena(dev)   # exists before any capture starts
         capturing = ar._capturing()
         if capturing:
             host, _ = ar.take(total)
-            host.copy_(torch.tensor(flat, dtype=torch.int32))
+            host.copy_(torch.from_numpy(flat) if isinstance(flat, np.ndarray)
+                       else torch.tensor(flat, dtype=torch.int32))
             packed = host.to(dev, non_blocking=True)
         else:
             packed = _ring(dev).stage(flat, dev)
@@ -257,6 +265,30 @@ def _tiles_host(sizes, block_m: int):
     return t_row0, t_rows, t_group
 
 
+def _np_ids(ids):
+    """Host expert ids (list, tuple or CPU tensor) as an int32 numpy array."""
+    if torch.is_tensor(ids):
+        return ids.to(torch.int32).numpy()
+    return np.asarray([int(e) for e in ids], dtype=np.int32)
+
+
+def _tiles_np(sizes_i, block_m: int):
+    """``_tiles_host`` as int32 numpy arrays (same tiles, same order), for
+    the launch paths: the host planning of a call stays a few numpy ops."""
+    m = np.asarray(sizes_i, dtype=np.int64)
+    cnt = (m + block_m - 1) // block_m
+    n = int(cnt.sum())
+    if n == 0:
+        z = np.zeros(0, dtype=np.int32)
+        return z, z, z
+    g = np.repeat(np.arange(len(m), dtype=np.int64), cnt)
+    first = np.cumsum(cnt) - cnt                          # first tile of each group
+    k = np.arange(n, dtype=np.int64) - first[g]           # tile index within its group
+    row0 = (np.cumsum(m) - m)[g] + k * block_m
+    rows = np.minimum(block_m, m[g] - k * block_m)
+    return row0.astype(np.int32), rows.astype(np.int32), g.astype(np.int32)
+
+
 def _xcd_balanced(t_row0, t_rows, t_group):
     """Order 256-row tiles for the four-wave kernels, which hand XCD x the
     x-th contiguous eighth of the tile list: the tiles, largest height class
@@ -268,6 +300,11 @@ def _xcd_balanced(t_row0, t_rows, t_group):
     n = len(t_row0)
     if n < 16:
         return t_row0, t_rows, t_group
+    if isinstance(t_rows, np.ndarray):
+        cls = (t_rows > 128).astype(np.int8) * 2 + ((t_rows > 64) & (t_rows <= 128))
+        ranked = np.concatenate([np.nonzero(cls == c)[0] for c in (2, 1, 0)])
+        order = np.concatenate([ranked[x::8] for x in range(8)])
+        return t_row0[order], t_rows[order], t_group[order]
     by_class = ([], [], [])
     for i, r in enumerate(t_rows):
         by_class[2 if r > 128 else (1 if r > 64 else 0)].append(i)
@@ -566,10 +603,10 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
             bm = _auto_block_m(max_m, K)
             if bm == 256 and not _tall_tiles_ok(N, K):
                 bm = _kernel_block_m(_prefill_block_m(max_m))
-        t0, tr, tg = _tiles_host(sizes_i, bm)
+        t0, tr, tg = _tiles_np(sizes_i, bm)
         if bm == 256:
             t0, tr, tg = _xcd_balanced(t0, tr, tg)
-        e_h, t0_d, tr_d, tg_d = to_device_i32((host_eids, t0, tr, tg), dev)
+        e_h, t0_d, tr_d, tg_d = to_device_i32((_np_ids(host_eids), t0, tr, tg), dev)
         eids = eids_dev if eids_dev is not None else e_h
         args = (eids.data_ptr(), None, G, t0_d.data_ptr(), tr_d.data_ptr(),
                 tg_d.data_ptr(), len(t0), bm)
@@ -613,16 +650,15 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     S = _scales_view(S)
     sizes_i = [int(m) for m in sizes]
     # tile height from the largest group, as in the forward (the kernel's
-    # per-row arithmetic does not depend on it); NF4 groups of more than 128
-    # rows take 256-row tiles (the four-wave transposed-read kernel)
+    # per-row arithmetic does not depend on it)
     bm = _dgrad_block_m(max(sizes_i), N, K)
-    t0, tr, tg = _tiles_host(sizes_i, bm)
+    t0, tr, tg = _tiles_np(sizes_i, bm)
     if bm == 256:
         t0, tr, tg = _xcd_balanced(t0, tr, tg)
     eids_dev = _eids_device(expert_ids, dev)
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
-    e_h, t0_d, tr_d, tg_d = to_device_i32(([] if eids_dev is not None else expert_ids,
+    e_h, t0_d, tr_d, tg_d = to_device_i32((_np_ids([] if eids_dev is not None else expert_ids),
                                            t0, tr, tg), dev)
     eids = eids_dev if eids_dev is not None else e_h
     with torch.cuda.device(dev):

@@ -165,3 +165,26 @@ def test_op_modules_do_not_import_the_oracle():
             elif isinstance(node, ast.ImportFrom):
                 names.add(node.module or "")
         assert not any(n.split(".")[0] == "oracle" for n in names), (mod.__name__, names)
+
+
+def test_numpy_tile_tables_equal_the_reference_tiling():
+    """The launch paths' numpy tile tables equal the list tiling (the
+    reference's build_group_tiles order), and the XCD ordering is the same
+    permutation on both forms."""
+    import numpy as np
+    from nf4_grouped import _tiles_host, _tiles_np, _xcd_balanced
+    rng = np.random.default_rng(5)
+    for trial in range(40):
+        G = int(rng.integers(0, 60))
+        sizes = [int(v) for v in rng.integers(0, 700, G)]
+        if trial % 5 == 0 and G:
+            sizes[0] = 0
+        for bm in (16, 32, 64, 128, 256):
+            ref = _tiles_host(sizes, bm)
+            got = _tiles_np(sizes, bm)
+            assert all(g.dtype == np.int32 for g in got)
+            assert [g.tolist() for g in got] == [list(r) for r in ref]
+            if bm == 256:
+                a = _xcd_balanced(*ref)
+                b = _xcd_balanced(*got)
+                assert [list(x) for x in a] == [y.tolist() for y in b]

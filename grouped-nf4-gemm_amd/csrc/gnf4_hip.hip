@@ -1565,7 +1565,8 @@ static_assert(kPwW0 + 3 * kPwWSlot <= kPwTab, "weight ring below the pair table"
 // scale of the lane's 32-column block and pairs rows with a byte permute.
 template <int FMT, int kM, bool DG>
 __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t, char* smem,
-                                               uint16_t* __restrict__ out, const int lut) {
+                                               uint16_t* __restrict__ out, const int lut,
+                                               const bool build_table) {
   const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
@@ -1854,7 +1855,8 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   issue_w(0, 0, 4);
   issue_a(0, 0, 8);
   // the NF4 pair table is built while the first loads are in flight
-  if constexpr (FMT == kNF4) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
+  if constexpr (FMT == kNF4)
+    if (build_table) init_pair_table16(reinterpret_cast<float2*>(smem + kPwTab), lut);
   // step 0's weight bytes and scales have landed (the activation pieces may
   // not have): their cache lines also hold the next steps' bytes and scales
   // of the same rows, so steps 1 and 2 hit in L2 instead of queueing a second
@@ -2021,27 +2023,36 @@ __global__ void __launch_bounds__(256, 1)
   const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
   __builtin_amdgcn_sched_barrier(0);
 
-  // this workgroup's tile: XCD x = blockIdx % 8 takes the x-th contiguous
-  // eighth of the tile list, in dispatch order
+  // XCD x = blockIdx % 8 takes the x-th contiguous eighth of the tile list;
+  // its workgroups walk that range with a stride of their count (tiles come
+  // largest first, so each workgroup gets one tile of every size band)
   const int n_tiles = (int)(((DG ? p.K : p.N) + kPfBN - 1) / kPfBN);
   const int64_t total = (int64_t)p.n_mtiles * n_tiles;
   const int nx = gridDim.x >= 8 ? 8 : 1;
   const int x = (int)(blockIdx.x % nx), idx = (int)(blockIdx.x / nx);
+  const int stride = (int)(gridDim.x / nx);
   const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
-  const int64_t tg = lo + idx;
-  if (tg >= hi) return;
-  PfTile t;
-  const int mt = (int)(tg / n_tiles);
-  t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
-  t.row0 = t_row0[mt];
-  t.rows = t_rows[mt];
-  t.e = eids[t_group[mt]];
-  if (t.rows > 128)
-    prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut);
-  else if (t.rows > 64)
-    prefill_w_tile<FMT, 4, DG>(p, t, smem, out, lut);
-  else
-    prefill_w_tile<FMT, 2, DG>(p, t, smem, out, lut);
+  bool first = true;
+  for (int64_t tg = lo + idx; tg < hi; tg += stride) {
+    if (!first) {
+      // every wave is past the previous tile's epilogue reads of the LDS
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+    }
+    PfTile t;
+    const int mt = (int)(tg / n_tiles);
+    t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
+    t.row0 = t_row0[mt];
+    t.rows = t_rows[mt];
+    t.e = eids[t_group[mt]];
+    if (t.rows > 128)
+      prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut, first);
+    else if (t.rows > 64)
+      prefill_w_tile<FMT, 4, DG>(p, t, smem, out, lut, first);
+    else
+      prefill_w_tile<FMT, 2, DG>(p, t, smem, out, lut, first);
+    first = false;
+  }
 }
 
 // ========================================================== tiled dgrad ==
@@ -2664,6 +2675,19 @@ bool prefill_enabled() {
   return on;
 }
 
+// Workgroups per XCD range of k_prefill_w: one per CU, each walking several
+// tiles (no per-tile dispatch, the pair table built once), or with
+// GNF4_PREFILL_PERSIST=0 one per tile.
+int64_t prefill_w_per_xcd(int64_t tiles, int cus) {
+  static const bool persist = [] {
+    const char* v = getenv("GNF4_PREFILL_PERSIST");
+    return !(v && v[0] == '0');
+  }();
+  const int64_t per_x = (tiles + 7) / 8;
+  const int64_t cap = cus >= 8 ? cus / 8 : 1;
+  return persist && per_x > cap ? cap : per_x;
+}
+
 // GNF4_PREFILL_W=0 keeps the eight-wave tall-tile kernel (k_prefill_t).
 bool prefill_w_enabled() {
   static const bool on = [] {
@@ -2688,8 +2712,8 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
       const int64_t grid = tiles < cus ? tiles : cus;
       if (prefill_w_enabled() && (int64_t)kPtBM * p.ldo * 2 < 0x7FFFFFFF) {
-        // one tile per workgroup; the grid covers eight equal XCD ranges
-        const int64_t per_x = (tiles + 7) / 8;
+        // the grid covers eight equal XCD ranges
+        const int64_t per_x = prefill_w_per_xcd(tiles, cus);
         if (per_x * 8 > 0x7FFFFFFF) return -1;
         hipLaunchKernelGGL((k_prefill_w<FMT>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream, p,
                            p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
@@ -2766,7 +2790,7 @@ int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
       f.K = p.K;
       f.ldo = p.ldo;
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.K + kPfBN - 1) / kPfBN);
-      const int64_t per_x = (tiles + 7) / 8;
+      const int64_t per_x = prefill_w_per_xcd(tiles, cus);
       if (per_x * 8 > 0x7FFFFFFF) return -1;
       hipLaunchKernelGGL((k_prefill_w<FMT, true>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream,
                          f, p.t_row0, p.t_rows, p.t_group, p.eids, p.out);

@@ -417,6 +417,32 @@ def pmc_workload(model):
         f"of {model.bytes_gu[0]} packed B")
 
 
+def pmc_prefill_workload(dev, seed=0):
+    """Kernels for the prefill HBM-traffic counter passes: the 256 MiB copy
+    (calibration), then config 4's gate_up and down calls (Zipf routing,
+    32768 rows), each three times, eagerly."""
+    import numpy as np
+    import torch
+    from nf4_grouped import gemm_4bit_grouped
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    (W, A), = make_nf4_layers(128, 1536, 2048, 1, dev, seed)
+    (W2, A2), = make_nf4_layers(128, 2048, 768, 1, dev, seed + 1)
+    sizes, ids = route(np.random.default_rng(seed), 4096, 8, 128, zipf_s=1.1)
+    T = sum(sizes)
+    x = torch.randn(T, 2048, device=dev).to(torch.bfloat16)
+    h = torch.randn(T, 768, device=dev).to(torch.bfloat16)
+    eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+    for a, Wt, At in ((x, W, A), (h, W2, A2)):
+        for _ in range(3):
+            gemm_4bit_grouped(a, Wt, At, sizes, eids)
+        torch.cuda.synchronize()
+    log(f"[bench] pmc prefill workload: 1 copy of {src.numel()} B, 3 gate_up + 3 down calls, {T} rows")
+
+
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed PMC
     summary, if present (line `traffic_bytes_per_launch: <int>`)."""
@@ -449,6 +475,9 @@ def main():
                     help="for rocprofv3 --pmc: one 256 MiB device copy (the counter "
                          "calibration), then the gate_up decode kernel of every layer, "
                          "launched eagerly twice; prints nothing else")
+    ap.add_argument("--pmc-prefill-workload", action="store_true",
+                    help="for rocprofv3 --pmc: the 256 MiB copy, then config 4's prefill "
+                         "gate_up and down calls, three each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -458,6 +487,9 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_prefill_workload:
+        pmc_prefill_workload(dev)
+        return
     if args.mma_workload:
         log(f"[bench] prefill {json.dumps(prefill_tflops(dev))}")
         log(f"[bench] dgrad {json.dumps(dgrad_tflops(dev))}")

@@ -1512,8 +1512,8 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // ==================================================== four-wave prefill ==
 //
 // k_prefill_w<FMT>: the tall-tile forward (256 token rows of one group x 256
-// weight rows per tile), one tile per 256-thread workgroup, one workgroup per
-// CU and one wave per SIMD. Each wave owns 64 weight rows (two 32-row MFMA
+// weight rows per tile), 256-thread workgroups, one workgroup per CU and one
+// wave per SIMD. Each wave owns 64 weight rows (two 32-row MFMA
 // blocks) for all 256 token rows, so
 //   * every activation operand read from LDS feeds two MFMAs (half the LDS
 //     operand traffic of a 32-row-per-wave split), and
@@ -1527,10 +1527,11 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // slice ("rolling" decode): during slice 0 of step f the wave decodes slice 3
 // of step f, during slices 1..3 it decodes slices 0..2 of step f + 1, each
 // into the operand registers the previous slice's MFMAs released.
-// One tile per workgroup: the hardware dispatcher hands the next tile to
-// whichever CU frees first, which balances ragged tiles. Tile ids are ordered
-// so each XCD (workgroup ids go to the XCDs round robin) works through a
-// contiguous range of the m-tile-major tile list.
+// The grid is persistent (by default one workgroup per CU): each XCD
+// (workgroup ids go to the XCDs round robin) works through a contiguous
+// range of the m-tile-major tile list, its workgroups taking every
+// (workgroups per XCD)-th tile of it; the NF4 pair table is built once per
+// workgroup.
 // The k order of every output element is that of k_prefill / k_prefill_t, so
 // all three give identical bits. Tiles of at most 128 or 64 rows skip the
 // MFMAs and operand reads of their empty 32-row subtiles.

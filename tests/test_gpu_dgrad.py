@@ -175,3 +175,22 @@ def test_dgrad_tall_mxfp4_scale_extremes():
     sub[:, :32] = (S[0, :, 0] == 0)[t % N].unsqueeze(1)
     assert torch.equal(got[~sub], want[~sub])
     assert bool(((got[sub] == want[sub]) | (got[sub] == 0)).all())
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_dgrad_tall_several_tiles_per_workgroup(fmt):
+    """40 groups of 300 one-hot rows x 4 output-column tiles: more tiles than
+    the persistent grid has workgroups, so workgroups run several 256- and
+    44-row tiles in turn. Row t of group g reproduces decoded row t % N of its
+    expert bit for bit."""
+    N, K, G, T = 128, 1024, 40, 300
+    W, S = _stack(fmt, G, N, K, seed=16)
+    ids = list(range(G - 1, -1, -1))
+    go = torch.zeros(G * T, N, dtype=torch.bfloat16, device="cuda")
+    t = torch.arange(G * T, device="cuda")
+    go[t, (t % T) % N] = 1
+    got = _ops()[fmt](go, W, S, [T] * G, ids)
+    for g in (0, 1, G // 2, G - 1):
+        dec = dequant(fmt, W[ids[g]], S[ids[g]]).to(torch.bfloat16)
+        rows = torch.arange(T, device="cuda")
+        assert torch.equal(got[g * T:(g + 1) * T], dec[rows % N]), g

@@ -411,3 +411,22 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
     sel = list(range(0, sum(sizes), 7))
     contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel),
                    [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_tall_tiles_several_per_workgroup(fmt):
+    """More 256-row tiles than the persistent grid has workgroups (64 groups
+    of mixed heights x 8 weight-row tiles), so each workgroup runs several
+    tiles of different row-subtile classes back to back, reusing its LDS and
+    pair table: bitwise equal to 128-row tiles and inside the contract."""
+    N, K, E = 2048, 256, 64
+    rng = np.random.default_rng(81)
+    sizes = [int(v) for v in rng.choice([300, 256, 200, 129, 128, 100, 65, 64, 40, 1], size=E)]
+    W, S = _stack(fmt, E, N, K, seed=82)
+    ids = [int(v) for v in rng.permutation(E)]
+    a = rand_acts(sum(sizes), K, seed=83)
+    op = _ops()[fmt]
+    tall = op(a, W, S, sizes, ids, block_m=256)
+    short = op(a, W, S, sizes, ids, block_m=128)
+    assert torch.equal(tall, short)
+    contract_check(fmt, tall, a, W, S, sizes, ids)

@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -31,6 +31,7 @@ SIGNATURES = {
     "gnf4_hip_activations_to_bf16": [_P, _I, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_ffn_sync_words": [_I, _I64, _I64],
+    "gnf4_hip_ffn_set_spin_limit": [_I],
     "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
                              _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],

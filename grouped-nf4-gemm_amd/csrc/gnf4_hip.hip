@@ -50,6 +50,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/gnf4_hip.h"
@@ -157,6 +158,68 @@ __device__ __forceinline__ void nf4_16bytes_to_bf16(const float2* tab, u32x4_t w
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int i = 0; i < 4; ++i) out[j][i] = bf16x2_bits(p[4 * j + i].x * s, p[4 * j + i].y * s);
+}
+
+// ---- exact three-part NF4 codebook (decode kernels) ----
+//
+// Every fp32 codebook value v splits exactly into three bf16 values,
+// v = hi + mid + lo: hi keeps the top 16 bits of v's pattern (sign, exponent,
+// 7 mantissa bits), the remainder r = v - hi is exact with at most 16
+// significant bits, mid keeps r's top 16 bits and lo = r - mid is exact with
+// at most 8 significant bits. Three bf16 MFMAs over the parts therefore sum
+// codebook values at full fp32 precision (each product of a bf16 activation
+// and a bf16 part is exact in fp32), and absmax multiplies the 64-element
+// block sum once, in fp32, as the reference's GEMV does
+// (kernel/nf4_grouped.py:508-511).
+//
+// The split table: 256 bytes x 16 lane columns x 16 B = 64 KiB. Entry (byte,
+// column) holds the bf16 pairs (part[byte >> 4], part[byte & 15]) of hi, mid
+// and lo in dwords 0..2 (element 2j, the high nibble, in the low half), so
+// one 16-byte LDS read decodes a byte into the three MFMA operand dwords.
+// Column = lane % 16: the 16 lanes of one LDS pass read distinct banks.
+constexpr int kSplitCols = 16;
+constexpr int kSplitTabBytes = 256 * kSplitCols * 16;
+static_assert(kSplitTabBytes == 8 * kPairEntries, "split and pair tables take the same LDS");
+
+__device__ __forceinline__ void nf4_split_parts(int lut, unsigned& himid, unsigned& lo) {
+  const unsigned u = (unsigned)lut;
+  const unsigned h = u & 0xFFFF0000u;
+  const float r = __uint_as_float(u) - __uint_as_float(h);          // exact
+  const unsigned rm = __float_as_uint(r) & 0xFFFF0000u;
+  const float l = r - __uint_as_float(rm);                           // exact
+  himid = (h >> 16) | rm;                  // hi in the low half, mid in the high half
+  lo = __float_as_uint(l) >> 16;
+}
+
+// Fill the split table from the codebook register of lanes 0..15 (see
+// nf4_lut_lane). Thread t fills byte t % 256; with 512 threads each byte's
+// 16 columns are split over two threads. Columns rotate with the byte so one
+// store instruction touches distinct banks.
+__device__ __forceinline__ void init_split_table(char* tab, int lut) {
+  unsigned hm, lo;
+  nf4_split_parts(lut, hm, lo);
+  const unsigned b = threadIdx.x & 255;
+  const unsigned hmh = __builtin_amdgcn_ds_bpermute((int)((b >> 4) << 2), (int)hm);
+  const unsigned hml = __builtin_amdgcn_ds_bpermute((int)((b & 15) << 2), (int)hm);
+  const unsigned loh = __builtin_amdgcn_ds_bpermute((int)((b >> 4) << 2), (int)lo);
+  const unsigned lol = __builtin_amdgcn_ds_bpermute((int)((b & 15) << 2), (int)lo);
+  const u32x4_t e = {(hmh & 0xFFFFu) | (hml << 16), (hmh >> 16) | (hml & 0xFFFF0000u),
+                     loh | (lol << 16), 0u};
+  const int nj = blockDim.x > 256 ? 8 : 16;
+  const int j0 = threadIdx.x < 256 ? 0 : 8;
+  for (int j = 0; j < nj; ++j)
+    *reinterpret_cast<u32x4_t*>(tab + b * (kSplitCols * 16) + (((j0 + j + b) & 15) * 16)) = e;
+}
+
+// 16-byte LDS read at a byte address: no base pointer arithmetic around it.
+typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4_t;
+__device__ __forceinline__ u32x4_t lds_read16(unsigned addr) {
+  return *(lds_u32x4_t*)(size_t)addr;
+}
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+typedef __attribute__((address_space(3))) const f32x2_t lds_f32x2_t;
+__device__ __forceinline__ f32x2_t lds_read8f(unsigned addr) {
+  return *(lds_f32x2_t*)(size_t)addr;
 }
 
 // 8 MXFP4 elements of one packed dword (low nibble first) -> 4 bf16 pairs.
@@ -280,8 +343,11 @@ constexpr int kPlain = 0, kFfnGu = 1, kFfnDn = 2;
 constexpr int kFfnFlagBase = 16;   // first flag word of the fused FFN's sync buffer
 
 struct NoWait {
-  __device__ void operator()() const {}
+  __device__ void operator()(int*) const {}
 };
+
+// Decode LDS: [table (NF4: 64 KiB)][status word, 16 B][activations][zero block]
+constexpr int kDecodeFlagBytes = 16;
 
 // The locked fp32 silu of the fused FFN: a fixed op sequence, no FMA
 // (this file builds with -ffp-contract=off), IEEE division. Same steps as
@@ -315,40 +381,78 @@ __device__ __forceinline__ float bf16_round(float f) {
 //   * with kAPieces > 0 (groups of at most two rows) the group's activation
 //     rows are staged once per workgroup into LDS (a few 16-byte loads per
 //     thread) in a [k / 8][row] layout and each MFMA A operand is a 16-byte
-//     LDS read (rows >= M read a zero block); with kAPieces == 0 (larger
-//     groups, where most lanes carry a row) the operands are loaded straight
-//     into registers with the weights;
+//     LDS read (rows that carry nothing read a zero block); with
+//     kAPieces == 0 (larger groups) the operands are loaded straight into
+//     registers with the weights;
 //   * each weight load moves 16 bytes per lane (32 elements of one row);
 //   * an NF4 lane's absmax values for a whole run are one 16-byte load;
-// and issues all of them before the first wait. The waves then reduce their
-// 16 x 16 partial tiles through LDS in wave order (deterministic). The
-// summation order of an output depends on K only, never on the unit kind or
-// on which tile the row sits in.
+// and issues all of them before the first wait.
 //
-// Dynamic LDS: [NF4 pair table 64 KiB][activations M * K * 2][zero block];
-// the reduction buffer reuses the start once the table is no longer read.
-// `lut` is the lane's codebook register (nf4_lut_lane). `ffn_h` is H for
-// kFfnGu. `wait_acts` runs, in every thread, after the first round's weight
-// loads are issued and before any activation load (kFfnDn).
+// NF4 rows of the MFMA output. A lane of quarter q holds 32 elements of a
+// 128-element chunk, so quarters 0-1 cover the chunk's first absmax block
+// and quarters 2-3 its second. The A operand keeps the blocks apart: A row r
+// carries token (r % 8) + 8 s of row set s, and only in the quarters of
+// block r / 8 (zeros elsewhere). Output rows 0-7 are then the first block's
+// sums and rows 8-15 the second's, which are exactly the rows the lane's
+// quarter holds (rows 4 q .. 4 q + 3), so each lane multiplies its chunk sums
+// by its own absmax in fp32 and accumulates them. Groups of up to 8 rows need
+// one row set, groups of up to 16 two (twice the MFMAs). The three codebook
+// parts (hi, mid, lo) go through three MFMAs per k-slice.
+// NF4 groups of one row (kSets == 0, the GEMV of decode proper) skip the
+// MFMA: each lane owns one weight row and 32 elements of one absmax block,
+// looks up fp32 codebook pairs in the pair table (init_pair_table), forms
+// the fp32 dot product with fp32 FMAs, and scales it by absmax once per
+// block -- the reference GEMV's arithmetic with all 64 lanes doing useful
+// work and no operand assembly.
+// MXFP4 keeps 16 token rows per MFMA: its weights are exact in bf16 and the
+// e8m0 scale is applied by the conversion instruction.
+//
+// The waves reduce their partial tiles through LDS in wave order
+// (deterministic); for NF4 each lane's value is the sum of its block-0 and
+// block-1 rows. The summation order of an output depends on K only, never on
+// the unit kind or on which tile the row sits in.
+//
+// Dynamic LDS: [NF4 split or pair table 64 KiB][status word][activations
+// M * K * 2][zero block]; the reduction buffer reuses the start once the
+// table is no longer read. `lut` is the lane's codebook register
+// (nf4_lut_lane). `ffn_h` is H and `ffn_epoch` the flag value of this call
+// for kFfnGu. `wait_acts(status)` runs, in every thread, after the first
+// round's weight loads are issued and before any activation load (kFfnDn);
+// it leaves a nonzero status word if the unit's inputs never became ready,
+// and the unit then writes NaN instead of its outputs.
 template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces, int kKind,
-          class Wait>
+          int kSets, class Wait>
 __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const int64_t nu,
                                             char* smem, const int lut, const int64_t ffn_h,
                                             const int64_t ffn_n_dn, uint32_t* ffn_sync,
-                                            const Wait& wait_acts) {
+                                            const uint32_t ffn_epoch, const Wait& wait_acts) {
   // kFfnDn reads h, written by other workgroups during this launch, with
   // device-scope loads
   constexpr int kActAux = kKind == kFfnDn ? kScopeDevice : 0;
   static_assert(kKind != kFfnGu || (FMT == kNF4 && kTiles == 2), "gate/up pairs need 2 tiles");
-  float2* s_tab = reinterpret_cast<float2*>(smem);
+  static_assert(kSets == 1 || (FMT == kNF4 && kSets == 2 && kAPieces == 0) ||
+                    (FMT == kNF4 && kSets == 0 && kAPieces > 0),
+                "row sets");
+  constexpr bool kOneRow = kSets == 0;
+  constexpr bool kSplit = FMT == kNF4 && !kOneRow;
+  constexpr int kSetsA = kSets > 0 ? kSets : 1;     // activation operand sets
   constexpr int kThreadsD = 64 * kDecodeWaves;
   constexpr bool kLateActs = kKind == kFfnDn;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nl = lane & 15;
   const int q = lane >> 4;
-  const unsigned lane_off = (unsigned)(lane & 31) * 8u;
+  // split table base (LDS address 0 here: bits 8..15 free for the byte) |
+  // lane column; one v_perm_b32 inserts the byte
+  // (pair table: 32 columns of 8 bytes)
+  const unsigned lane_off =
+      (unsigned)(uintptr_t)smem |
+      (kOneRow ? (unsigned)(lane & 31) * 8u : (unsigned)(lane & (kSplitCols - 1)) * 16u);
   constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+  // NF4: A row nl carries token (nl & 7) (+ 8 per row set) in the quarters of
+  // block nl / 8 only
+  const bool blk_lane = !kSplit || ((nl < 8) == (q < 2));
+  const int tok = kSplit ? (nl & 7) : nl;
 
   // the expert id and the group's rows in one round trip of scalar loads
   // (their latency heads every weight load): a null row_off reads the id
@@ -374,7 +478,8 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   if (M <= 0) return;  // uniform across the workgroup (empty group)
   const int K32 = (int)p.K;
   const int kslices = K32 >> 3;                       // 16-byte activation pieces per row
-  const int a_base = FMT == kNF4 ? 8 * kPairEntries : 0;
+  int* const s_status = reinterpret_cast<int*>(smem + (FMT == kNF4 ? kSplitTabBytes : 0));
+  const int a_base = (FMT == kNF4 ? kSplitTabBytes : 0) + kDecodeFlagBytes;
   const int zero_off = a_base + ((M * kslices * 16 + 15) & ~15);
 
   // ---- activation staging loads (first in the queue: they are waited on first)
@@ -407,9 +512,15 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   }
   const int nchunks = (K32 + 127) >> 7;
 
-  f32x4_t acc[kTiles][2];
+  // MXFP4: two accumulators per tile (alternate k-slices). NF4: one fp32
+  // accumulator per tile and row set, fed with absmax-scaled chunk sums.
+  // One row: acc[t][0][0] is the lane's (row, quarter) partial.
+  constexpr int kAcc = kSplit ? kSets : kOneRow ? 1 : 2;
+  f32x4_t acc[kTiles][kAcc];
 #pragma unroll
-  for (int t = 0; t < kTiles; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+    for (int s = 0; s < kAcc; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // One round: this wave's chunks c0 .. c0 + kChunksPerWave - 1. All loads
   // first; in the first round the LDS staging (table, activations) happens
@@ -421,10 +532,10 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
     u32x4_t wb[kChunksPerWave][kTiles];
     unsigned sb[kChunksPerWave][kTiles];
     u32x4_t sv[kTiles];
-    u32x4_t ab[kAPieces == 0 ? kChunksPerWave : 1][4];
+    u32x4_t ab[kAPieces == 0 ? kChunksPerWave : 1][kSetsA][4];
     if constexpr (FMT == kNF4) {
       // absmax blocks 2 * c0 .. 2 * c0 + 3 of the lane's row: chunk c0 + i,
-      // segment q uses block 2 * (c0 + i) + q / 2
+      // quarter q uses block 2 * (c0 + i) + q / 2
       const bool sval = (unsigned)(c0 * 128) < (unsigned)K32;
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
@@ -435,11 +546,15 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
     auto act_loads = [&](int i) {
       if constexpr (kAPieces == 0) {
         const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
-        const bool kval = kseg < (unsigned)K32;
-        // rows >= M fall outside the activation resource and load as zeros
-        const int aoff = oob_unless(kval, (int)((int64_t)nl * p.lda * 2) + (int)kseg * 2);
+        const bool kval = kseg < (unsigned)K32 && blk_lane;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ab[i][j] = buf_load16_aux<kActAux>(ra, aoff + 16 * j);
+        for (int s = 0; s < kSets; ++s) {
+          // rows >= M fall outside the activation resource and load as zeros
+          const int aoff = oob_unless(
+              kval, (int)((int64_t)(tok + 8 * s) * p.lda * 2) + (int)kseg * 2);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ab[i][s][j] = buf_load16_aux<kActAux>(ra, aoff + 16 * j);
+        }
       }
     };
 #pragma unroll
@@ -455,7 +570,7 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
       if constexpr (!late) act_loads(i);
     }
     if constexpr (late) {
-      wait_acts();
+      wait_acts(s_status);
       stage_loads();
 #pragma unroll
       for (int i = 0; i < kChunksPerWave; ++i) act_loads(i);
@@ -471,7 +586,8 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
         }
     }
     if constexpr (first) {
-      if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
+      if constexpr (kSplit) init_split_table(smem, lut);
+      if constexpr (kOneRow) init_pair_table(reinterpret_cast<float2*>(smem), lut);
       if (kAPieces > 0 && threadIdx.x < 4)
         *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -488,32 +604,86 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
     for (int i = 0; i < kChunksPerWave; ++i) {
       const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
       const bool kval = kseg < (unsigned)K32;
-      u32x4_t a[4];
-      if constexpr (kAPieces > 0) {
+      u32x4_t a[kSetsA][4];
+      if constexpr (kOneRow) {
+        // every lane: the group's one row over its 32 elements
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[0][j] = *reinterpret_cast<const u32x4_t*>(
+              smem + (kval ? a_base + ((int)(kseg >> 3) + j) * 16 : zero_off));
+      } else if constexpr (kAPieces > 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int off =
-              (kval && nl < M) ? a_base + (((int)(kseg >> 3) + j) * M + nl) * 16 : zero_off;
-          a[j] = *reinterpret_cast<const u32x4_t*>(smem + off);
+          const int off = (kval && blk_lane && tok < M)
+                              ? a_base + (((int)(kseg >> 3) + j) * M + tok) * 16
+                              : zero_off;
+          a[0][j] = *reinterpret_cast<const u32x4_t*>(smem + off);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = ab[i][j];
+        for (int s = 0; s < kSets; ++s)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[s][j] = ab[i][s][j];
       }
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) {
-        u32x4_t b[4];
-        if constexpr (FMT == kNF4) {
-          nf4_16bytes_to_bf16(s_tab, wb[i][t], lane_off, __uint_as_float(sb[i][t]), b);
+        if constexpr (kOneRow) {
+          // fp32 codebook pairs times fp32 activations, four chains
+          float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              const unsigned addr =
+                  __builtin_amdgcn_perm(wb[i][t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8));
+              const f32x2_t w = lds_read8f(addr);
+              const unsigned x = a[0][j][b];
+              d[2 * (b & 1)] = __builtin_fmaf(w[0], __uint_as_float(x << 16), d[2 * (b & 1)]);
+              d[2 * (b & 1) + 1] =
+                  __builtin_fmaf(w[1], __uint_as_float(x & 0xFFFF0000u), d[2 * (b & 1) + 1]);
+            }
+          acc[t][0][0] = __builtin_fmaf((d[0] + d[1]) + (d[2] + d[3]),
+                                        __uint_as_float(sb[i][t]), acc[t][0][0]);
+        } else if constexpr (kSplit) {
+          // chunk sums of the three parts, two chains per row set
+          f32x4_t c[kSets][2];
+#pragma unroll
+          for (int s = 0; s < kSets; ++s) c[s][0] = c[s][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            u32x4_t d[4];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              const unsigned addr =
+                  __builtin_amdgcn_perm(wb[i][t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8));
+              d[b] = lds_read16(addr);
+            }
+            const u32x4_t hi = {d[0][0], d[1][0], d[2][0], d[3][0]};
+            const u32x4_t mid = {d[0][1], d[1][1], d[2][1], d[3][1]};
+            const u32x4_t lo = {d[0][2], d[1][2], d[2][2], d[3][2]};
+#pragma unroll
+            for (int s = 0; s < kSets; ++s) {
+              c[s][j & 1] = mfma(a[s][j], hi, c[s][j & 1]);
+              c[s][j & 1] = mfma(a[s][j], mid, c[s][j & 1]);
+              c[s][j & 1] = mfma(a[s][j], lo, c[s][j & 1]);
+            }
+          }
+          const float am = __uint_as_float(sb[i][t]);
+#pragma unroll
+          for (int s = 0; s < kSets; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              acc[t][s][r] = __builtin_fmaf(c[s][0][r] + c[s][1][r], am, acc[t][s][r]);
         } else {
+          u32x4_t b[4];
           const float sc = e8m0_to_f32(sb[i][t]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) b[j] = mx_dword_to_bf16(wb[i][t][j], sc);
+          acc[t][0] = mfma(a[0][0], b[0], acc[t][0]);
+          acc[t][1] = mfma(a[0][1], b[1], acc[t][1]);
+          acc[t][0] = mfma(a[0][2], b[2], acc[t][0]);
+          acc[t][1] = mfma(a[0][3], b[3], acc[t][1]);
         }
-        acc[t][0] = mfma(a[0], b[0], acc[t][0]);
-        acc[t][1] = mfma(a[1], b[1], acc[t][1]);
-        acc[t][0] = mfma(a[2], b[2], acc[t][0]);
-        acc[t][1] = mfma(a[3], b[3], acc[t][1]);
       }
     }
   };
@@ -524,33 +694,73 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
     round(c0, std::false_type{});
 
   __syncthreads();  // the table is no longer read: its space takes the partials
-  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem);   // [kDecodeWaves][kTiles][64]
+  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem);   // [kDecodeWaves][kTiles][kSetsA][64]
+  float* s_red1 = reinterpret_cast<float*>(smem);      // one row: [kDecodeWaves][kTiles][64]
 #pragma unroll
-  for (int t = 0; t < kTiles; ++t) s_red[(wave * kTiles + t) * 64 + lane] = acc[t][0] + acc[t][1];
+  for (int t = 0; t < kTiles; ++t) {
+    if constexpr (kOneRow) {
+      s_red1[(wave * kTiles + t) * 64 + lane] = acc[t][0][0];
+    } else {
+#pragma unroll
+      for (int s = 0; s < kSetsA; ++s) {
+        if constexpr (kSplit)
+          s_red[((wave * kTiles + t) * kSetsA + s) * 64 + lane] = acc[t][s];
+        else
+          s_red[((wave * kTiles + t) * kSetsA + s) * 64 + lane] = acc[t][0] + acc[t][kAcc - 1];
+      }
+    }
+  }
   __syncthreads();
+  // tile t, row set s of the output, summed over the waves in wave order;
+  // NF4 lanes 0..31 add the second block's rows (lane + 32) to the first's;
+  // one row: lanes 0..15 add the four quarters of their row (element 0)
+  auto reduced = [&](int t, int s) {
+    if constexpr (kOneRow) {
+      const float* r = s_red1 + t * 64 + nl;
+      constexpr int kStride = kTiles * 64;
+      float v = (r[0] + r[16]) + (r[32] + r[48]);
+#pragma unroll
+      for (int w = 1; w < kDecodeWaves; ++w)
+        v = v + ((r[w * kStride] + r[w * kStride + 16]) + (r[w * kStride + 32] + r[w * kStride + 48]));
+      return f32x4_t{v, 0.f, 0.f, 0.f};
+    } else {
+      const f32x4_t* r = s_red + (t * kSetsA + s) * 64 + lane;
+      constexpr int kStride = kTiles * kSetsA * 64;
+      f32x4_t v = kSplit ? r[0] + r[32] : r[0];
+#pragma unroll
+      for (int w = 1; w < kDecodeWaves; ++w)
+        v = v + (kSplit ? r[w * kStride] + r[w * kStride + 32] : r[w * kStride]);
+      return v;
+    }
+  };
+  // output rows of lane (nl, q), i = 0..3: 8 s + 4 q + i (NF4, q < 2), 4 q + i
+  // (MXFP4), or row 0 of lanes 0..15 (one row)
+  const bool writer = kOneRow ? lane < 16 : (!kSplit || q < 2);
+  constexpr int kRowsPerLane = kOneRow ? 1 : 4;
   if constexpr (kKind == kFfnGu) {
     // wave 0 sums the gate and up tiles over the waves in wave order and
     // writes h for its 16 columns: the same bits as a plain gu launch
     // (bf16 out) followed by the silu-multiply kernel
     if (wave == 0) {
-      f32x4_t vg = s_red[lane], vu = s_red[64 + lane];
-#pragma unroll
-      for (int w = 1; w < kDecodeWaves; ++w) {
-        vg = vg + s_red[(w * kTiles) * 64 + lane];
-        vu = vu + s_red[(w * kTiles + 1) * 64 + lane];
-      }
       // h goes out with device-scope stores; once the wave's stores have
       // completed (vmcnt 0) they are visible to device-scope loads on every
-      // XCD, and lane 0 counts the unit for its group
+      // XCD
       const __amdgpu_buffer_rsrc_t rh =
           make_rsrc(p.out + (int64_t)r0 * p.ldo, (int64_t)M * p.ldo * 2);
       const int col = (int)(nu * 16 + nl);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = 4 * q + i;
-        const float hv = silu_locked(bf16_round(vg[i])) * bf16_round(vu[i]);
-        const int off = oob_unless(m < M, (int)(((int64_t)m * p.ldo + col) * 2));
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(hv), rh, off, 0, kScopeDevice);
+      for (int s = 0; s < kSetsA; ++s) {
+        const f32x4_t vg = reduced(0, s), vu = reduced(1, s);
+        if (writer) {
+#pragma unroll
+          for (int i = 0; i < kRowsPerLane; ++i) {
+            const int m = 8 * s + 4 * q + i;
+            const float hv = silu_locked(bf16_round(vg[i])) * bf16_round(vu[i]);
+            const int off = oob_unless(m < M, (int)(((int64_t)m * p.ldo + col) * 2));
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(hv), rh, off, 0,
+                                                  kScopeDevice);
+          }
+        }
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       // one flag in the private row of every down unit of the group:
@@ -559,22 +769,24 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
       const int64_t dn_per_group = (ffn_n_dn + 31) / 32;
       uint32_t* row0 = ffn_sync + kFfnFlagBase + (int64_t)g * dn_per_group * gu_per_group + nu;
       for (int64_t d = lane; d < dn_per_group; d += 64)
-        __hip_atomic_store(row0 + d * gu_per_group, 1u, __ATOMIC_RELAXED,
+        __hip_atomic_store(row0 + d * gu_per_group, ffn_epoch, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
   } else {
-    // wave t < kTiles sums tile t over the waves in wave order (deterministic)
-    if (wave < kTiles) {
-      const int t = wave;
+    // a down unit whose h never became ready writes NaN (the status word was
+    // set before the barrier that ended its wait)
+    const bool poisoned = kLateActs && *s_status != 0;
+    // wave t * kSetsA + s sums tile t, row set s over the waves
+    if (wave < kTiles * kSetsA) {
+      const int t = wave / kSetsA, s = wave - t * kSetsA;
       const int64_t n = (nu * kTiles + t) * 16 + nl;
-      f32x4_t v = s_red[t * 64 + lane];
+      const f32x4_t v = reduced(t, s);
+      if (writer && n < p.N) {
 #pragma unroll
-      for (int w = 1; w < kDecodeWaves; ++w) v = v + s_red[(w * kTiles + t) * 64 + lane];
-      if (n < p.N) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * q + i;
-          if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+        for (int i = 0; i < kRowsPerLane; ++i) {
+          const int m = (kSplit ? 8 * s : 0) + 4 * q + i;
+          if (m < M)
+            p.out[(int64_t)(r0 + m) * p.ldo + n] = poisoned ? (uint16_t)0x7FC0 : f32_to_bf16_bits(v[i]);
         }
       }
     }
@@ -582,7 +794,7 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
 }
 
 // Decode path: one unit per workgroup.
-template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces>
+template <int FMT, int kChunksPerWave, int kTiles, int kDecodeWaves, int kAPieces, int kSets>
 // two workgroups per CU: kDecodeWaves / 2 waves per SIMD
 // The grid is (units per group, G): the unit is read off the block
 // coordinates, with no division (G <= 65535 on this path).
@@ -598,8 +810,8 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
                "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
                "s"(q.ldo));
   const int g = (int)blockIdx.y;   // < G: the grid has exactly G rows of units
-  decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain>(
-      q, g, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, NoWait{});
+  decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain, kSets>(
+      q, g, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, 0u, NoWait{});
 }
 
 // ------------------------------------------------------------ fused FFN --
@@ -608,30 +820,37 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
 // launch. Workgroups [0, G * H / 16) are gate/up units, the rest are down
 // units (G * ceil(N_dn / 32)), both in group-major order. A down unit only
 // waits on gate/up units, which have smaller ids; workgroups are dispatched
-// in id order and gate/up units never wait, so the wait always ends. (A bounded spin backs this up: a unit that polls
-// kFfnSpinLimit times sets the error word and goes on.)
+// in id order and gate/up units never wait, so the wait always ends. A
+// bounded spin backs this up: a down unit that polls `spin_limit` times
+// without seeing its flags sets the error word, writes NaN into its output
+// rows instead of a result, and exits.
 //
 // Hand-off without cache maintenance or atomics: a gate/up unit writes its
 // 16 columns of h (bf16, [T, ldh]) with device-scope stores, waits for them
-// to complete, and then sets its flag in the private flag row of every down
-// unit of its group (device-scope stores). A down unit issues its weight
-// loads, polls its own row with one device-scope vector load until every
-// flag is set, reads h with device-scope loads, and clears its row: it is
-// the row's only reader, so the words are zero again for the next call (and
-// for graph replays) without any counting. Release/acquire fences would
-// write back or invalidate whole L2 caches per unit, and same-address
-// atomics serialise at about 0.1 us each; both cost more than the launch
-// this saves.
+// to complete, and then writes this call's epoch (a nonzero per-call value)
+// into its flag in the private flag row of every down unit of its group
+// (device-scope stores). A down unit issues its weight loads, polls its own
+// row with one device-scope vector load until every flag holds the epoch,
+// reads h with device-scope loads, and clears its row: it is the row's only
+// reader, so the words are zero again for the next call (and for graph
+// replays) without any counting. A flag left behind by a call that timed
+// out holds an older epoch, which no later call's down unit accepts.
+// Release/acquire fences would write back or invalidate whole L2 caches per
+// unit, and same-address atomics serialise at about 0.1 us each; both cost
+// more than the launch this saves.
 //
 // Sync words (u32, device memory, zero before the first call): [0] error
-// flag, then G * ceil(N_dn / 32) rows of H / 16 flags from word
-// kFfnFlagBase. Calls that overlap on one sync buffer race.
-constexpr int kFfnSpinLimit = 1 << 22;   // polls before a down unit gives up
+// flag (sticky: set by a timed-out down unit, cleared only by the caller),
+// then G * ceil(N_dn / 32) rows of H / 16 flags from word kFfnFlagBase.
+// Calls that overlap on one sync buffer race.
+constexpr int kFfnSpinLimit = 1 << 22;   // default polls before a down unit gives up
 constexpr int kFfnMaxDynLds = 160 * 1024;
 
-template <int CPW1, int CPW2, int kAPieces>
+template <int CPW1, int CPW2, int kAPieces, int kSets>
 __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const FwdArgs dn,
-                                                       const int64_t H, uint32_t* sync) {
+                                                       const int64_t H, uint32_t* sync,
+                                                       const uint32_t epoch,
+                                                       const int spin_limit) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int lut = nf4_lut_lane();
   __builtin_amdgcn_sched_barrier(0);
@@ -645,8 +864,8 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
   if (u < gu_units) {
     // unit counts stay below 2^31 (the launch checks): 32-bit division
     const int gg = (int)((uint32_t)u / (uint32_t)gu_per_group);
-    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu>(gu, gg, u - (int64_t)gg * gu_per_group, smem,
-                                                     lut, H, dn.N, sync, NoWait{});
+    decode_unit<kNF4, CPW1, 2, 8, kAPieces, kFfnGu, kSets>(
+        gu, gg, u - (int64_t)gg * gu_per_group, smem, lut, H, dn.N, sync, epoch, NoWait{});
     return;
   }
   const int64_t d = u - gu_units;
@@ -654,16 +873,18 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
   const int M = dn.row_off ? dn.row_off[g + 1] - dn.row_off[g] : 1;
   if (M <= 0) return;                   // empty group: no gate/up unit sets its flags
   uint32_t* row = sync + kFfnFlagBase + d * gu_per_group;
-  auto wait_h = [&]() {
+  auto wait_h = [&](int* status) {
     if (threadIdx.x < 64) {             // wave 0 polls the row, 64 flags per load
       const int lane = threadIdx.x;
       int spins = 0;
+      bool timed_out = false;
       while (true) {
         bool all = true;
         for (int64_t j = lane; j < gu_per_group; j += 64)
-          all &= __hip_atomic_load(row + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+          all &= __hip_atomic_load(row + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
         if (__builtin_amdgcn_ballot_w64(!all) == 0) break;
-        if (++spins > kFfnSpinLimit) {   // not expected: flag it and go on
+        if (++spins > spin_limit) {     // not expected: flag it, poison the outputs
+          timed_out = true;
           if (lane == 0)
             __hip_atomic_store(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
@@ -672,14 +893,15 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
       }
       for (int64_t j = lane; j < gu_per_group; j += 64)   // this row's only reader
         __hip_atomic_store(row + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) *status = timed_out ? 1 : 0;
     }
     // no wave issues an h load before wave 0 has seen every flag (the weight
-    // loads already in flight need not land first)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    // loads already in flight need not land first); the status word is
+    // visible to every wave after the barrier
+    __syncthreads();
   };
-  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn>(dn, g, d - (int64_t)g * dn_per_group, smem, lut,
-                                                   0, 0, sync, wait_h);
+  decode_unit<kNF4, CPW2, 2, 8, kAPieces, kFfnDn, kSets>(dn, g, d - (int64_t)g * dn_per_group, smem,
+                                                         lut, 0, 0, sync, 0u, wait_h);
 }
 
 // Elementwise silu-multiply for the unfused path (and groups too large for
@@ -1233,256 +1455,9 @@ __global__ void __launch_bounds__(512, 2)
   }
 }
 
-// Tall variant of k_prefill: 256-row tiles. The decoded weights of a step
-// (each lane: 32 k of one weight row, decoded once) feed eight 32-row
-// activation subtiles instead of four, so the VALU decode per MFMA halves --
-// on gfx950 the VALU and the matrix core barely overlap within a SIMD, which
-// makes decode VALU per MFMA the step's second cost after the MFMAs. A tile
-// of at most 128 rows (a group's tail) runs only the lower four subtiles.
-// LDS: the NF4 pair table (64 KiB, static, so its base folds into the
-// instructions' offset field) and three 32 KiB activation stages; kS = 3, so
-// the step loop unrolls over six steps to keep the decode double buffer's
-// parity static.
+// 256-row tiles (k_prefill_w below).
 constexpr int kPtBM = 256;
 constexpr int kPtStage = kPtBM * kPfBK * 2;
-
-template <int FMT>
-__global__ void __launch_bounds__(512, 2)
-    k_prefill_t(const FwdArgs p, const int32_t* __restrict__ t_row0,
-                const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
-                const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
-  constexpr int kS = 3;
-  constexpr int kWaves = 8;
-  constexpr int kWaveCols = kPfBN / kWaves;          // 32
-  constexpr int kAPieces = kPtStage / 1024 / kWaves; // 4
-  constexpr int kRowsPerWave = kPtBM / kWaves;       // 32
-  constexpr int kGroupLoads = kAPieces + 2;
-  constexpr int kMT = kPtBM / 32;                    // 8
-  static_assert(kWaveCols == 32, "one weight subtile per wave");
-  __shared__ __attribute__((aligned(16))) float2 s_tab[FMT == kNF4 ? kPairEntries : 2];
-  __shared__ __attribute__((aligned(16))) char s_a0[kPtStage];
-  __shared__ __attribute__((aligned(16))) char s_a1[kPtStage];
-  __shared__ __attribute__((aligned(16))) char s_a2[kPtStage];
-  auto stage_of = [&](auto RI) -> char* {
-    constexpr int r = decltype(RI)::value;
-    if constexpr (r == 0) return s_a0;
-    else if constexpr (r == 1) return s_a1;
-    else return s_a2;
-  };
-  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
-  __builtin_amdgcn_sched_barrier(0);
-  const int lane = threadIdx.x & 63, wave = uniform(threadIdx.x >> 6);
-  const int l32 = lane & 31, h = lane >> 5;
-  const unsigned lane_off = (unsigned)(lane & 31) * 8u;
-  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
-
-  const int n_tiles = (int)((p.N + kPfBN - 1) / kPfBN);
-  const int64_t total = (int64_t)p.n_mtiles * n_tiles;
-  const int nx = gridDim.x >= 8 ? 8 : 1;
-  const int x = (int)(blockIdx.x % nx), slot = (int)(blockIdx.x / nx);
-  const int wpx = (int)((gridDim.x - x + nx - 1) / nx);
-  const int64_t lo = total * x / nx, hi = total * (x + 1) / nx;
-  const int my_tiles = lo + slot < hi ? (int)((hi - lo - slot + wpx - 1) / wpx) : 0;
-  const int ksteps = (int)((p.K + kPfBK - 1) / kPfBK);
-  const int F = my_tiles * ksteps;
-  if constexpr (FMT == kNF4) init_pair_table(s_tab, lut);
-  if (F == 0) return;
-
-  auto meta = [&](int j) {
-    PfTile t;
-    const int64_t tg = lo + slot + (int64_t)j * wpx;
-    const int mt = (int)(tg / n_tiles);
-    t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
-    t.row0 = t_row0[mt];
-    t.rows = t_rows[mt];
-    t.e = eids[t_group[mt]];
-    return t;
-  };
-
-  const int64_t lda2 = p.lda * 2;
-  int a_row[kAPieces], a_slot[kAPieces];
-#pragma unroll
-  for (int i = 0; i < kAPieces; ++i) {
-    a_row[i] = wave * kRowsPerWave + i * 8 + (lane >> 3);
-    a_slot[i] = (lane & 7) ^ pf_swz(a_row[i] & 15);
-  }
-  int a_off[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) a_off[kk] = l32 * 128 + ((4 * h + kk) ^ pf_swz(l32 & 15)) * 16;
-
-  u32x4_t wreg[kS];
-  unsigned sreg[kS];
-  PfTile ring_t[kS];
-  bool ring_last[kS];
-  f32x16_t acc[kMT];
-#pragma unroll
-  for (int i = 0; i < kMT; ++i) acc[i] = f32x16_t{};
-
-  int iss_j = 0, iss_ks = 0;
-  PfTile iss_t;
-  const char* a_base = nullptr;
-  const uint8_t* b_base = nullptr;
-  const char* s_base = nullptr;
-  int a_bytes = 0, b_bytes = 0, s_bytes = 0;
-  int a_voff[kAPieces], b_voff = 0, s_voff = 0;
-  auto tile_setup = [&](int j) {
-    iss_t = meta(j);
-    a_base = reinterpret_cast<const char*>(p.a + (int64_t)iss_t.row0 * p.lda);
-    a_bytes = (int)((int64_t)iss_t.rows * lda2);
-#pragma unroll
-    for (int i = 0; i < kAPieces; ++i)
-      a_voff[i] = a_row[i] < iss_t.rows ? (int)(a_row[i] * lda2) + a_slot[i] * 16 : kOOB;
-    b_base = p.B + (int64_t)iss_t.e * p.sbe;
-    b_bytes = (int)(p.N * p.sbn);
-    s_base = static_cast<const char*>(p.S) + (int64_t)iss_t.e * p.sse * kScaleBytes;
-    s_bytes = (int)(p.N * p.ssn * kScaleBytes);
-    const int64_t n = iss_t.n0 + wave * kWaveCols + l32;
-    b_voff = n < p.N ? (int)(n * p.sbn) + h * 16 : kOOB;
-    if constexpr (FMT == kNF4) s_voff = n < p.N ? (int)(n * p.ssn * 4) : kOOB;
-    else s_voff = n < p.N ? (int)(n * p.ssn) + h : kOOB;
-  };
-  tile_setup(0);
-
-  auto issue = [&](auto RI, char* stage, bool live) {
-    constexpr int r = decltype(RI)::value;
-    const int k0 = uniform(iss_ks) * kPfBK;
-    live = uniform(live ? 1 : 0) != 0;
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        uniform_ptr(a_base), 0, uniform(live ? a_bytes : 0), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        uniform_ptr(b_base), 0, uniform(live ? b_bytes : 0), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        uniform_ptr(s_base), 0, uniform(live ? s_bytes : 0), 0x00020000);
-#pragma unroll
-    for (int i = 0; i < kAPieces; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (lds_ptr_t)(stage + (wave * kAPieces + i) * 1024), 16, a_voff[i], k0 * 2, 0, 0);
-    wreg[r] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, b_voff, k0 >> 1, 0));
-    if constexpr (FMT == kNF4)
-      sreg[r] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff, (k0 >> 6) * 4, 0);
-    else
-      sreg[r] = __builtin_amdgcn_raw_buffer_load_b8(rs, s_voff, k0 >> 5, 0);
-    ring_t[r] = iss_t;
-    ring_last[r] = iss_ks == ksteps - 1;
-    if (++iss_ks == ksteps) {
-      iss_ks = 0;
-      ++iss_j;
-      if (iss_j < my_tiles) tile_setup(iss_j);
-    }
-  };
-
-  // wf: the current step's decoded operands; the next step's are decoded
-  // into the same registers once this step's MFMAs have issued.
-  u32x4_t wf[4];
-  auto decode = [&](auto RI) {
-    constexpr int r = decltype(RI)::value;
-    if constexpr (FMT == kNF4) {
-      const float sc = __uint_as_float(sreg[r]);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) wf[kk] = nf4_dword_to_bf16(s_tab, wreg[r][kk], lane_off, sc);
-    } else {
-      const float sc = e8m0_to_f32(sreg[r]);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) wf[kk] = mx_dword_to_bf16(wreg[r][kk], sc);
-    }
-  };
-
-  // MFMAs of a step over the first kM activation subtiles (parity q's
-  // weights); the first k-slice's MFMAs are followed by `after_first`.
-  // One operand register per subtile: subtile i's operand for slice kk + 1
-  // is read right after slice kk's MFMA on it issues, and the slice's
-  // remaining MFMAs cover the LDS latency. `full` == false (a tail tile of at
-  // most 128 rows) skips the upper four subtiles; only their MFMAs and reads
-  // sit under the (uniform) branch.
-  auto mma = [&](bool full, const char* stage, auto&& after_first) {
-    constexpr int kHalf = kMT / 2;
-    u32x4_t av[kMT];
-#pragma unroll
-    for (int i = 0; i < kHalf; ++i)
-      av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[0] + i * 4096);
-    if (full) {
-#pragma unroll
-      for (int i = kHalf; i < kMT; ++i)
-        av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[0] + i * 4096);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int i = 0; i < kHalf; ++i) {
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[kk]), as_bf16x8(av[i]),
-                                                          acc[i], 0, 0, 0);
-        if (kk + 1 < 4)
-          av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk + 1] + i * 4096);
-      }
-      if (full) {
-#pragma unroll
-        for (int i = kHalf; i < kMT; ++i) {
-          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wf[kk]), as_bf16x8(av[i]),
-                                                            acc[i], 0, 0, 0);
-          if (kk + 1 < 4)
-            av[i] = *reinterpret_cast<const u32x4_t*>(stage + a_off[kk + 1] + i * 4096);
-        }
-      }
-      if (kk == 0) {
-        __builtin_amdgcn_sched_barrier(0);
-        after_first();
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
-
-  auto compute = [&](auto RI, const char* stage, auto&& after_first) {
-    constexpr int r = decltype(RI)::value;
-    constexpr int rn = (r + 1) % kS;
-    const int rows = uniform(ring_t[r].rows);
-    // a tail tile of at most 128 rows skips the upper four subtiles
-    mma(rows > kPtBM / 2, stage, after_first);
-    __builtin_amdgcn_sched_barrier(0);
-    decode(std::integral_constant<int, rn>{});
-    if (ring_last[r]) {
-      const PfTile t = ring_t[r];
-      const int n_l = t.n0 + wave * kWaveCols + 4 * h;
-      uint16_t* o = out + (int64_t)(t.row0 + l32) * p.ldo + n_l;
-#pragma unroll
-      for (int i = 0; i < kMT; ++i) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (i * 32 + l32 < rows && n_l + 8 * g < p.N) {
-            uint2 v;
-            v.x = bf16x2_bits(acc[i][4 * g + 0], acc[i][4 * g + 1]);
-            v.y = bf16x2_bits(acc[i][4 * g + 2], acc[i][4 * g + 3]);
-            *reinterpret_cast<uint2*>(o + (int64_t)i * 32 * p.ldo + 8 * g) = v;
-          }
-        }
-        acc[i] = f32x16_t{};
-      }
-    }
-  };
-
-  // Step f uses ring slot f % 3.
-  int f = 0;
-  auto step = [&](auto RI) {
-    constexpr int r = decltype(RI)::value;
-    constexpr int rf = (r + kS - 1) % kS;
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vm_lgkm0<(kS - 2) * kGroupLoads>();
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    const bool live = f + kS - 1 < F;
-    compute(RI, stage_of(RI), [&]() {
-      issue(std::integral_constant<int, rf>{}, stage_of(std::integral_constant<int, rf>{}), live);
-    });
-    return ++f < F;
-  };
-
-  issue(std::integral_constant<int, 0>{}, s_a0, true);
-  issue(std::integral_constant<int, 1>{}, s_a1, F > 1);
-  if constexpr (FMT == kNF4) __syncthreads();  // pair table complete
-  decode(std::integral_constant<int, 0>{});
-  auto st = [&](auto RI) { return step(RI); };
-  while (StepUnroll<0, kS>::run(st)) {
-  }
-}
 
 // Pair table with 16 columns: entry (byte b, column c) at b * 128 + c * 8.
 __device__ __forceinline__ void init_pair_table16(float2* tab, int lut) {
@@ -1532,8 +1507,8 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // range of the m-tile-major tile list, its workgroups taking every
 // (workgroups per XCD)-th tile of it; the NF4 pair table is built once per
 // workgroup.
-// The k order of every output element is that of k_prefill / k_prefill_t, so
-// all three give identical bits. Tiles of at most 128 or 64 rows skip the
+// The k order of every output element is that of k_prefill, so both give
+// identical bits. Tiles of at most 128 or 64 rows skip the
 // MFMAs and operand reads of their empty 32-row subtiles.
 //
 // LDS map: activation stages at 0, 32 and 64 KiB; weight ring at 96 KiB
@@ -2529,29 +2504,45 @@ int device_cus() {
 int64_t clamp_grid(int64_t work, int64_t cap) { return work < cap ? (work > 0 ? work : 1) : cap; }
 
 // Launch one decode-kernel instance with `lds` bytes of dynamic LDS.
-template <int FMT, int CPW, int T, int W, int PA>
+template <int FMT, int CPW, int T, int W, int PA, int S>
 int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream) {
   static int configured_dev = -1;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -2;
   if (configured_dev != dev) {   // allow more than the default 64 KiB of dynamic LDS
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode_fwd<FMT, CPW, T, W, PA>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode_fwd<FMT, CPW, T, W, PA, S>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
       return -2;
     configured_dev = dev;
   }
-  hipLaunchKernelGGL((k_decode_fwd<FMT, CPW, T, W, PA>), grid, dim3(64 * W), lds, stream, p);
+  hipLaunchKernelGGL((k_decode_fwd<FMT, CPW, T, W, PA, S>), grid, dim3(64 * W), lds, stream, p);
   return 0;
 }
 
+// pa: LDS-staged activation pieces per thread (0: register operands);
+// sets: NF4 row sets (0: one-row groups on the fp32 FMA path, 2 when a group
+// has more than 8 rows)
 template <int FMT, int CPW, int T>
-int launch_decode_pa(const FwdArgs& p, dim3 grid, int pa, int lds, hipStream_t stream) {
+int launch_decode_pa(const FwdArgs& p, dim3 grid, int pa, int sets, int lds, hipStream_t stream) {
   constexpr int W = 8;
+  if constexpr (FMT == kNF4) {
+    if (sets == 0) {
+      switch (pa) {
+        case 1: return launch_decode_inst<FMT, CPW, T, W, 1, 0>(p, grid, lds, stream);
+        case 2: return launch_decode_inst<FMT, CPW, T, W, 2, 0>(p, grid, lds, stream);
+        case 4: return launch_decode_inst<FMT, CPW, T, W, 4, 0>(p, grid, lds, stream);
+        default: return -1;
+      }
+    }
+  }
   switch (pa) {
-    case 1: return launch_decode_inst<FMT, CPW, T, W, 1>(p, grid, lds, stream);
-    case 2: return launch_decode_inst<FMT, CPW, T, W, 2>(p, grid, lds, stream);
-    case 4: return launch_decode_inst<FMT, CPW, T, W, 4>(p, grid, lds, stream);
-    default: return launch_decode_inst<FMT, CPW, T, W, 0>(p, grid, lds, stream);
+    case 1: return launch_decode_inst<FMT, CPW, T, W, 1, 1>(p, grid, lds, stream);
+    case 2: return launch_decode_inst<FMT, CPW, T, W, 2, 1>(p, grid, lds, stream);
+    case 4: return launch_decode_inst<FMT, CPW, T, W, 4, 1>(p, grid, lds, stream);
+    default:
+      if constexpr (FMT == kNF4)
+        if (sets == 2) return launch_decode_inst<FMT, CPW, T, W, 0, 2>(p, grid, lds, stream);
+      return launch_decode_inst<FMT, CPW, T, W, 0, 1>(p, grid, lds, stream);
   }
 }
 
@@ -2573,19 +2564,20 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   const int64_t a_bytes = stage ? (int64_t)p.max_m * p.K * 2 : 0;
   const int64_t pieces = (a_bytes + 15) / 16;
   const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
-  const int64_t red = (int64_t)kW * kT * 64 * 16;
-  const int64_t table = FMT == kNF4 ? 8 * kPairEntries : 0;
-  int64_t lds = table + ((a_bytes + 15) & ~15) + 64;
+  const int sets = FMT != kNF4 ? 1 : p.max_m > 8 ? 2 : (p.max_m == 1 && pa > 0) ? 0 : 1;
+  const int64_t red = (int64_t)kW * kT * (sets > 0 ? sets : 1) * 64 * 16;
+  const int64_t table = FMT == kNF4 ? kSplitTabBytes : 0;
+  int64_t lds = table + kDecodeFlagBytes + ((a_bytes + 15) & ~15) + 64;
   if (lds < red) lds = red;
   if (lds > 160 * 1024) return -1;
-  if (per_wave <= 1) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, (int)lds, stream);
+  if (per_wave <= 1) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, sets, (int)lds, stream);
   if constexpr (FMT == kNF4) {
-    return launch_decode_pa<FMT, 2, kT>(p, grid, pa, (int)lds, stream);
+    return launch_decode_pa<FMT, 2, kT>(p, grid, pa, sets, (int)lds, stream);
   } else {
-    if (per_wave <= 2) return launch_decode_pa<FMT, 2, kT>(p, grid, pa, (int)lds, stream);
+    if (per_wave <= 2) return launch_decode_pa<FMT, 2, kT>(p, grid, pa, 1, (int)lds, stream);
     if (per_wave <= 3 || !stage)   // register operands: 3 chunks per round fit 128 VGPRs
-      return launch_decode_pa<FMT, 3, kT>(p, grid, pa, (int)lds, stream);
-    return launch_decode_pa<FMT, 4, kT>(p, grid, pa, (int)lds, stream);
+      return launch_decode_pa<FMT, 3, kT>(p, grid, pa, 1, (int)lds, stream);
+    return launch_decode_pa<FMT, 4, kT>(p, grid, pa, 1, (int)lds, stream);
   }
 }
 
@@ -2614,36 +2606,64 @@ int launch_decode(const FwdArgs& p, hipStream_t stream) {
 
 // Fused FFN decode launch (every group at most 16 rows). Phase shapes:
 // gate/up over K, down over H; the chunk split per wave follows each K.
-template <int CPW1, int CPW2, int PA>
-int launch_ffn_inst(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
+// Sync words and per-call values of a fused FFN launch.
+struct FfnSync {
+  uint32_t* words;
+  uint32_t epoch;      // nonzero; differs between consecutive launches
+  int spin_limit;
+};
+
+// Per-process launch counter for the flag epochs, and the spin limit of
+// later launches (gnf4_hip_ffn_set_spin_limit).
+std::atomic<uint32_t> g_ffn_epoch{0};
+std::atomic<int> g_ffn_spin_limit{kFfnSpinLimit};
+
+uint32_t next_ffn_epoch() {
+  uint32_t e = g_ffn_epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (e == 0) e = g_ffn_epoch.fetch_add(1, std::memory_order_relaxed) + 1;   // 0 means clear
+  return e;
+}
+
+template <int CPW1, int CPW2, int PA, int S>
+int launch_ffn_inst(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& fs,
                     uint32_t n_units, int lds, hipStream_t stream) {
   static int configured_dev = -1;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -2;
   if (configured_dev != dev) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ffn_decode<CPW1, CPW2, PA>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_ffn_decode<CPW1, CPW2, PA, S>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kFfnMaxDynLds) !=
         hipSuccess)
       return -2;
     configured_dev = dev;
   }
-  hipLaunchKernelGGL((k_ffn_decode<CPW1, CPW2, PA>), dim3(n_units), dim3(512), lds, stream,
-                     gu, dn, H, sync);
+  hipLaunchKernelGGL((k_ffn_decode<CPW1, CPW2, PA, S>), dim3(n_units), dim3(512), lds, stream,
+                     gu, dn, H, fs.words, fs.epoch, fs.spin_limit);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 template <int CPW1, int CPW2>
-int launch_ffn_pa(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
-                  uint32_t n_units, int pa, int lds, hipStream_t stream) {
+int launch_ffn_pa(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& fs,
+                  uint32_t n_units, int pa, int sets, int lds, hipStream_t stream) {
+  if (sets == 0) {
+    switch (pa) {
+      case 1: return launch_ffn_inst<CPW1, CPW2, 1, 0>(gu, dn, H, fs, n_units, lds, stream);
+      case 2: return launch_ffn_inst<CPW1, CPW2, 2, 0>(gu, dn, H, fs, n_units, lds, stream);
+      case 4: return launch_ffn_inst<CPW1, CPW2, 4, 0>(gu, dn, H, fs, n_units, lds, stream);
+      default: return -1;
+    }
+  }
   switch (pa) {
-    case 1: return launch_ffn_inst<CPW1, CPW2, 1>(gu, dn, H, sync, n_units, lds, stream);
-    case 2: return launch_ffn_inst<CPW1, CPW2, 2>(gu, dn, H, sync, n_units, lds, stream);
-    case 4: return launch_ffn_inst<CPW1, CPW2, 4>(gu, dn, H, sync, n_units, lds, stream);
-    default: return launch_ffn_inst<CPW1, CPW2, 0>(gu, dn, H, sync, n_units, lds, stream);
+    case 1: return launch_ffn_inst<CPW1, CPW2, 1, 1>(gu, dn, H, fs, n_units, lds, stream);
+    case 2: return launch_ffn_inst<CPW1, CPW2, 2, 1>(gu, dn, H, fs, n_units, lds, stream);
+    case 4: return launch_ffn_inst<CPW1, CPW2, 4, 1>(gu, dn, H, fs, n_units, lds, stream);
+    default:
+      if (sets == 2) return launch_ffn_inst<CPW1, CPW2, 0, 2>(gu, dn, H, fs, n_units, lds, stream);
+      return launch_ffn_inst<CPW1, CPW2, 0, 1>(gu, dn, H, fs, n_units, lds, stream);
   }
 }
 
-int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
+int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& fs,
                hipStream_t stream) {
   constexpr int kW = 8;
   const int64_t units = (int64_t)gu.G * (H / 16) + (int64_t)gu.G * ((dn.N + 31) / 32);
@@ -2654,48 +2674,27 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, uint32_t* sync,
   const int64_t a_bytes = stage ? (int64_t)gu.max_m * kmax * 2 : 0;
   const int64_t pieces = (a_bytes + 15) / 16;
   const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
-  int64_t lds = 8 * kPairEntries + ((a_bytes + 15) & ~15) + 64;
-  const int64_t red = (int64_t)kW * 2 * 64 * 16;
+  const int sets = gu.max_m > 8 ? 2 : (gu.max_m == 1 && pa > 0) ? 0 : 1;
+  int64_t lds = kSplitTabBytes + kDecodeFlagBytes + ((a_bytes + 15) & ~15) + 64;
+  const int64_t red = (int64_t)kW * 2 * (sets > 0 ? sets : 1) * 64 * 16;
   if (lds < red) lds = red;
   if (lds > kFfnMaxDynLds) return -1;
   const bool two1 = ((gu.K + 127) / 128 + kW - 1) / kW > 1;
   const bool two2 = ((dn.K + 127) / 128 + kW - 1) / kW > 1;
   const uint32_t n = (uint32_t)units;
-  if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
-  if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, sync, n, pa, (int)lds, stream);
-  if (two2) return launch_ffn_pa<1, 2>(gu, dn, H, sync, n, pa, (int)lds, stream);
-  return launch_ffn_pa<1, 1>(gu, dn, H, sync, n, pa, (int)lds, stream);
+  if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
+  if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
+  if (two2) return launch_ffn_pa<1, 2>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
+  return launch_ffn_pa<1, 1>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
 }
 
-// GNF4_PREFILL=0 selects the simpler tiled kernel (k_gemm_fwd) instead.
-bool prefill_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("GNF4_PREFILL");
-    return !(v && v[0] == '0');
-  }();
-  return on;
-}
-
-// Workgroups per XCD range of k_prefill_w: one per CU, each walking several
-// tiles (no per-tile dispatch, the pair table built once), or with
-// GNF4_PREFILL_PERSIST=0 one per tile.
+// Workgroups per XCD range of the persistent k_prefill_w grid: one per CU
+// (each walks several tiles; the pair table is built once per workgroup), or
+// fewer when the XCD's range has fewer tiles.
 int64_t prefill_w_per_xcd(int64_t tiles, int cus) {
-  static const bool persist = [] {
-    const char* v = getenv("GNF4_PREFILL_PERSIST");
-    return !(v && v[0] == '0');
-  }();
   const int64_t per_x = (tiles + 7) / 8;
   const int64_t cap = cus >= 8 ? cus / 8 : 1;
-  return persist && per_x > cap ? cap : per_x;
-}
-
-// GNF4_PREFILL_W=0 keeps the eight-wave tall-tile kernel (k_prefill_t).
-bool prefill_w_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("GNF4_PREFILL_W");
-    return !(v && v[0] == '0');
-  }();
-  return on;
+  return per_x > cap ? cap : per_x;
 }
 
 template <int FMT>
@@ -2709,23 +2708,20 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
     const bool pf_ok = p.N % 4 == 0 && p.ldo % 4 == 0 && p.K % kPfBK == 0 &&
                        (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPtBM &&
                        (int64_t)kPtBM * p.lda * 2 < 0x7FFFFFFF;
-    if (pf_ok && prefill_enabled() && block_m == kPtBM) {
+    if (block_m == kPtBM) {
+      // 256-row tiles: the host picks them only where the four-wave kernel
+      // takes the shape
+      if (!pf_ok || (int64_t)kPtBM * p.ldo * 2 >= 0x7FFFFFFF) return -1;
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
-      const int64_t grid = tiles < cus ? tiles : cus;
-      if (prefill_w_enabled() && (int64_t)kPtBM * p.ldo * 2 < 0x7FFFFFFF) {
-        // the grid covers eight equal XCD ranges
-        const int64_t per_x = prefill_w_per_xcd(tiles, cus);
-        if (per_x * 8 > 0x7FFFFFFF) return -1;
-        hipLaunchKernelGGL((k_prefill_w<FMT>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream, p,
-                           p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
-        return hipGetLastError() == hipSuccess ? 0 : -2;
-      }
-      hipLaunchKernelGGL((k_prefill_t<FMT>), dim3((unsigned)grid), dim3(512), 0, stream, p,
+      // the grid covers eight equal XCD ranges
+      const int64_t per_x = prefill_w_per_xcd(tiles, cus);
+      if (per_x * 8 > 0x7FFFFFFF) return -1;
+      hipLaunchKernelGGL((k_prefill_w<FMT>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream, p,
                          p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
       return hipGetLastError() == hipSuccess ? 0 : -2;
     }
     if (block_m > kPfBM) return -1;
-    if (pf_ok && prefill_enabled()) {
+    if (pf_ok) {
       const int64_t tiles = (int64_t)p.n_mtiles * ((p.N + kPfBN - 1) / kPfBN);
       int64_t grid = tiles < cus ? tiles : cus;
       const int dyn = FMT == kNF4 ? 8 * kPairEntries : 0;
@@ -2755,15 +2751,6 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-// GNF4_DGRAD_W=0 keeps dgrad on k_dgrad_tiled (at most 128-row tiles).
-bool dgrad_w_enabled() {
-  static const bool on = [] {
-    const char* v = getenv("GNF4_DGRAD_W");
-    return !(v && v[0] == '0');
-  }();
-  return on;
-}
-
 template <int FMT>
 int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   const int cus = device_cus();
@@ -2776,7 +2763,7 @@ int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
                       (int64_t)kPtBM * p.ldg * 2 < 0x7FFFFFFF &&
                       (int64_t)kPtBM * p.ldo * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF &&
                       p.N * p.ssn * 4 < 0x7FFFFFFF;
-    if (w_ok && prefill_enabled() && dgrad_w_enabled()) {
+    if (w_ok) {
       FwdArgs f{};
       f.a = p.g;
       f.lda = p.ldg;
@@ -2801,7 +2788,8 @@ int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
   const bool tiled_ok = p.N % kDgStep == 0 && p.ldo % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
                         (int64_t)kPfBM * p.ldg * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF;
-  if (tiled_ok && prefill_enabled()) {
+  if (block_m > kPfBM) return -1;
+  if (tiled_ok) {
     FwdArgs f{};
     f.a = p.g;
     f.lda = p.ldg;
@@ -2953,6 +2941,12 @@ int gnf4_hip_silu_mul(const void* gu, int64_t ldg, int64_t T, int64_t H, void* h
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
+int gnf4_hip_ffn_set_spin_limit(int polls) {
+  if (polls < 0) return -1;
+  g_ffn_spin_limit.store(polls, std::memory_order_relaxed);
+  return 0;
+}
+
 int64_t gnf4_hip_ffn_sync_words(int G, int64_t N_gu, int64_t N_dn) {
   if (G < 0 || N_gu <= 0 || N_dn <= 0) return -1;
   return kFfnFlagBase + (int64_t)G * ((N_dn + 31) / 32) * (N_gu / 32);
@@ -3013,7 +3007,8 @@ int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t*
   dn.out = static_cast<uint16_t*>(out);
   dn.ldo = ldo;
   if (device_cus() <= 0) return -2;
-  return launch_ffn(gu, dn, H, sync, static_cast<hipStream_t>(stream));
+  const FfnSync fs{sync, next_ffn_epoch(), g_ffn_spin_limit.load(std::memory_order_relaxed)};
+  return launch_ffn(gu, dn, H, fs, static_cast<hipStream_t>(stream));
 }
 
 int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,

@@ -11,9 +11,12 @@ first H outputs, up = the last H), ``dn_packed [E, N_dn, H/2]`` u8 +
 Two paths, both HIP:
   * every group at most 16 rows (decode): ONE launch of the fused kernel.
     gate/up units write the intermediate h straight from their epilogue and
-    signal a per-group counter; down units stream their weights meanwhile
-    and start the moment their group's h is complete. No gu tensor is
-    written, and there is no second or third launch.
+    set per-call flags for the down units of their group; down units stream
+    their weights meanwhile and start the moment their group's h is
+    complete. No gu tensor is written, and there is no second or third
+    launch. A down unit that never sees its flags (not expected) writes NaN
+    into its output rows and sets a sticky error word
+    (``ffn_sync_error()``).
   * larger groups: the tiled forward kernel for gate_up, the silu-multiply
     kernel, the tiled forward kernel for down.
 
@@ -50,33 +53,59 @@ def _fused_units(G: int, H: int, n_dn: int) -> int:
 
 
 _SYNC_LOCK = threading.Lock()
-_SYNC = {}   # (device index, stream handle) -> int32 sync words, zero between calls
+_SYNC = {}      # (device index, stream handle) -> current int32 sync words
+_RETIRED = []   # outgrown sync buffers: never freed (a captured graph may use them)
 
 
 def _sync_words(dev, G: int, n_gu: int, n_dn: int):
     """The fused kernel's sync words for this device and stream. They start
-    at zero and every call leaves them at zero, so one buffer serves every
-    stream-ordered call; a separate buffer per stream keeps concurrent
-    streams apart."""
+    at zero and every call leaves its flags at zero, so one buffer serves
+    every stream-ordered call; a separate buffer per stream keeps concurrent
+    streams apart. A call that needs more words gets a larger buffer; the
+    old one is kept alive for the life of the process, because a graph
+    captured earlier still holds its address (graph captures share one
+    capture stream, hence one key)."""
     key = (dev.index, _stream_ptr(dev))
     need = int(_hiplib.load().gnf4_hip_ffn_sync_words(G, n_gu, n_dn))
     with _SYNC_LOCK:
         buf = _SYNC.get(key)
         if buf is None or buf.numel() < need:
+            if buf is not None:
+                _RETIRED.append(buf)
             buf = torch.zeros(max(need, 4096), dtype=torch.int32, device=dev)
             _SYNC[key] = buf
     return buf
 
 
-def ffn_sync_error(device=None) -> bool:
-    """True if a down unit of any fused call on this device gave up waiting
-    for its h (the output of that call is invalid). Reads device memory: it
-    synchronises, so it is meant for tests and diagnostics."""
+def _device_buffers(device):
     dev = torch.device(device if device is not None else "cuda")
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
     with _SYNC_LOCK:
-        bufs = [b for (d, _s), b in _SYNC.items() if d == idx]
-    return any(int(b[0].item()) != 0 for b in bufs)
+        return ([b for (d, _s), b in _SYNC.items() if d == idx]
+                + [b for b in _RETIRED if b.device.index == idx])
+
+
+def ffn_sync_error(device=None) -> bool:
+    """True if a down unit of any fused call on this device gave up waiting
+    for its h since the last ``ffn_sync_clear`` (that call's affected output
+    rows are NaN). Reads device memory: it synchronises, so it is meant for
+    tests and diagnostics."""
+    return any(int(b[0].item()) != 0 for b in _device_buffers(device))
+
+
+def ffn_sync_clear(device=None) -> None:
+    """Zero every sync buffer of this device (error word and flags): after
+    an error, graph replays of fused calls are valid again only after this.
+    Stream-ordered on the current stream; no fused call may be in flight on
+    another stream."""
+    for b in _device_buffers(device):
+        b.zero_()
+
+
+def set_spin_limit(polls: int) -> None:
+    """Polls a down unit of later fused launches makes before it gives up
+    (default 2**22). For diagnostics and tests of the time-out path."""
+    _hiplib.check(_hiplib.load().gnf4_hip_ffn_set_spin_limit(int(polls)), "set_spin_limit")
 
 
 def silu_mul_locked(gu: torch.Tensor) -> torch.Tensor:

@@ -11,15 +11,22 @@ back to memory. Both call hand-written HIP kernels (``csrc/gnf4_hip.hip``)
 through the C ABI in ``include/gnf4_hip.h``; there is no CPU, Triton or
 eager-PyTorch fallback. On a non-GPU tensor the ops raise.
 
-Numerics: every weight is decoded as ``bf16(fp32(NF4[code] * absmax))`` (one
-fp32 rounding, one bf16 rounding -- the same values ``dequant_ref(...)`` gives
-after ``.to(bfloat16)``), products are exact in the bf16 MFMA and accumulate
-in fp32, and each output is rounded to bf16 once. fp16 and fp32 activations
-are first rounded to bf16 (nearest-even), so their result equals the
-forward of ``a.to(bfloat16)`` bit for bit. The reference's Triton
-mainloop uses TF32 operands instead; the stated bound is the tolerance
-contract (reference docs/TOLERANCE_CONTRACT.md): B-rel <= 2x the bf16
-dequant-then-matmul path against an fp64 reference, and <= 1e-2.
+Numerics. Decode (every group of at most 16 rows) keeps the codebook in
+fp32, as the reference's GEMV does (kernel/nf4_grouped.py:508-511): each
+64-element block's dot product of fp32 codebook values and bf16 activations
+is formed in fp32 and scaled by absmax once, in fp32. One-row groups use
+fp32 FMAs; larger groups put an exact three-part bf16 split of the codebook
+through three bf16 MFMAs. The tiled kernels (larger groups) use bf16 weights
+``bf16(fp32(NF4[code] * absmax))`` -- the same values ``dequant_ref(...)``
+gives after ``.to(bfloat16)``, the reference's opt-in VARIANT 3
+(kernel/nf4_grouped.py:438-445) -- into bf16 MFMA with fp32 accumulation.
+Every output is rounded to bf16 once. fp16 and fp32 activations are first
+rounded to bf16 (nearest-even), so their result equals the forward of
+``a.to(bfloat16)`` bit for bit. The stated bound is the tolerance contract
+(reference docs/TOLERANCE_CONTRACT.md): B-rel <= 2x the bf16
+dequant-then-matmul path against an fp64 reference, <= 1e-2, and the
+fidelity ordering P-fid (decode strictly below the dequant path's error,
+tiles tied with it).
 """
 from __future__ import annotations
 
@@ -416,10 +423,21 @@ def _auto_block_m(max_rows: int, K: int = 0) -> int:
 
 def _tall_tiles_ok(N: int, K: int) -> bool:
     """Whether the library takes 256-row forward tiles for this shape (whole
-    64-wide k steps, 4-column output stores; ``GNF4_PREFILL=0`` in the
-    environment turns the tiled MFMA kernels off)."""
-    return (K % 64 == 0 and N % 4 == 0
-            and os.environ.get("GNF4_PREFILL", "1")[:1] != "0")
+    64-wide k steps, 4-column output stores)."""
+    return K % 64 == 0 and N % 4 == 0
+
+
+def _fwd_block_m(max_m: int, N: int, K: int, block_m=None) -> int:
+    """Tile height of a tiled forward launch, shared by the op and by
+    ``GroupPlan``: the caller's ``block_m`` rounded up to a supported
+    height, else ``_auto_block_m`` where the shape takes 256-row tiles, else
+    the reference's group-size rule."""
+    if block_m is not None:
+        return _kernel_block_m(block_m)
+    bm = _auto_block_m(max_m, K)
+    if bm == 256 and not _tall_tiles_ok(N, K):
+        bm = _kernel_block_m(_prefill_block_m(max_m))
+    return bm
 
 
 # ------------------------------------------------------------------ launch --
@@ -500,44 +518,56 @@ class GroupPlan:
     """Device-resident group tables for repeated calls with the same routing
     (e.g. inside a captured graph or a timing loop): the expert ids, row
     offsets or tile table are uploaded once, so a planned call launches the
-    kernel with no host-to-device copy. Not part of the reference's API."""
+    kernel with no host-to-device copy. Not part of the reference's API.
 
-    def __init__(self, sizes, expert_ids, device, block_m=None):
+    The tiled path's tile height depends on the weights' shape (as in the
+    op, ``_fwd_block_m``); its tables are built on the first planned launch
+    for a shape, or up front for ``shape=(N, K)``. A graph capture must be
+    preceded by one eager planned launch per shape (uploads synchronise)."""
+
+    def __init__(self, sizes, expert_ids, device, block_m=None, shape=None):
         sizes_i = [int(m) for m in sizes]
+        self.sizes = sizes_i
         self.G = len(sizes_i)
         self.max_m = max(sizes_i) if sizes_i else 0
         self.one_row_each = bool(sizes_i) and min(sizes_i) == 1 and self.max_m == 1
-        dev = torch.device(device)
+        self.device = torch.device(device)
         ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else list(expert_ids)
         self.max_id = max((int(e) for e in ids), default=-1)
         self.min_id = min((int(e) for e in ids), default=0)
+        self.user_block_m = block_m
         self.decode = self.max_m <= DECODE_MAX_ROWS and block_m is None
+        self.eids = torch.tensor(ids, dtype=torch.int32, device=self.device)
+        self._tables = {}
         if self.decode:
             row_off = [0]
             for m in sizes_i:
                 row_off.append(row_off[-1] + m)
-            self.eids, self.row_off = (torch.tensor(ids, dtype=torch.int32, device=dev),
-                                       torch.tensor(row_off, dtype=torch.int32, device=dev))
-            self.tables = None
-            self.block_m = self.max_m
+            self.row_off = torch.tensor(row_off, dtype=torch.int32, device=self.device)
         else:
-            self.block_m = (_kernel_block_m(block_m) if block_m is not None
-                            else _auto_block_m(self.max_m))
-            t0, tr, tg = _tiles_host(sizes_i, self.block_m)
-            if self.block_m == 256:
-                t0, tr, tg = _xcd_balanced(t0, tr, tg)
-            self.eids = torch.tensor(ids, dtype=torch.int32, device=dev)
             self.row_off = None
-            self.tables = tuple(torch.tensor(v, dtype=torch.int32, device=dev) for v in (t0, tr, tg))
-        self.n_mtiles = 0 if self.decode else self.tables[0].numel()
+            if shape is not None:
+                self.tables(*shape)
 
-    def args(self):
+    def tables(self, N: int, K: int):
+        """(block_m, (t_row0, t_rows, t_group) on the device) for a weight
+        shape: the tile height the op would use."""
+        bm = _fwd_block_m(self.max_m, N, K, self.user_block_m)
+        if bm not in self._tables:
+            t0, tr, tg = _tiles_host(self.sizes, bm)
+            if bm == 256:
+                t0, tr, tg = _xcd_balanced(t0, tr, tg)
+            self._tables[bm] = tuple(torch.tensor(v, dtype=torch.int32, device=self.device)
+                                     for v in (t0, tr, tg))
+        return bm, self._tables[bm]
+
+    def args(self, N: int, K: int):
         if self.decode:
             ro = None if self.one_row_each else self.row_off.data_ptr()
             return (self.eids.data_ptr(), ro, self.G, None, None, None, 0, self.max_m)
-        t0, tr, tg = self.tables
+        bm, (t0, tr, tg) = self.tables(N, K)
         return (self.eids.data_ptr(), None, self.G, t0.data_ptr(), tr.data_ptr(), tg.data_ptr(),
-                self.n_mtiles, self.block_m)
+                t0.numel(), bm)
 
 
 def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
@@ -556,7 +586,7 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
         rc = lib.gnf4_hip_grouped_fwd(
             fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
             W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
-            *plan.args(), N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+            *plan.args(N, K), N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
     _hiplib.check(rc, "launch_planned")
     return out
 
@@ -597,12 +627,7 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
         # decode path: block_m carries the largest group size
         args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, max_m)
     else:
-        if block_m is not None:
-            bm = _kernel_block_m(block_m)
-        else:
-            bm = _auto_block_m(max_m, K)
-            if bm == 256 and not _tall_tiles_ok(N, K):
-                bm = _kernel_block_m(_prefill_block_m(max_m))
+        bm = _fwd_block_m(max_m, N, K, block_m)
         t0, tr, tg = _tiles_np(sizes_i, bm)
         if bm == 256:
             t0, tr, tg = _xcd_balanced(t0, tr, tg)
@@ -626,11 +651,8 @@ def _dgrad_block_m(max_rows: int, N: int, K: int) -> int:
     """Tile height of a dgrad launch: 256-row tiles when the four-wave
     transposed-read kernel takes the shape (whole 64-wide n steps and k
     blocks), else the forward's group-size rule capped at 128 rows (the
-    eight-wave dgrad kernels). ``GNF4_DGRAD_W=0`` or ``GNF4_PREFILL=0`` in
-    the environment (read by the library too) keep the eight-wave kernels."""
-    four_wave = (os.environ.get("GNF4_DGRAD_W", "1")[:1] != "0"
-                 and os.environ.get("GNF4_PREFILL", "1")[:1] != "0")
-    if max_rows > 128 and four_wave and N % 64 == 0 and K % 64 == 0:
+    eight-wave dgrad kernels)."""
+    if max_rows > 128 and N % 64 == 0 and K % 64 == 0:
         return 256
     return _kernel_block_m(_prefill_block_m(max_rows))
 

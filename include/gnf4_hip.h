@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 4
+#define GNF4_HIP_ABI_VERSION 5
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -130,10 +130,15 @@ int gnf4_hip_silu_mul(const void *gu, int64_t ldg, int64_t T, int64_t H, void *h
  *   W_dn  [E, N_dn, H/2] u8 + absmax [E, N_dn, H/64] f32.
  *   h     [T, ldh] bf16 workspace (the intermediate; ldh >= H, % 8 == 0).
  *   sync  >= gnf4_hip_ffn_sync_words(G, N_gu, N_dn) u32 words, zero
- *         before the first call; every call leaves them zero again (graph
- *         replays included). Calls that overlap on one sync buffer race.
- *         Word 0 becomes nonzero if a down unit gave up waiting for h (never
- *         expected; the output is then invalid).
+ *         before the first call; every call leaves its flags zero again
+ *         (graph replays included). Calls that overlap on one sync buffer
+ *         race. Word 0 is a sticky error flag: it becomes nonzero if a down
+ *         unit gave up waiting for h (never expected), and that unit's
+ *         output rows are NaN. Flags carry a per-call epoch, so flags left
+ *         behind by such a call are never taken for a later call's; graph
+ *         replays reuse the epoch captured with them, so after an error a
+ *         replayed graph's result is invalid until the caller clears the
+ *         sync buffer.
  *   out   [T, ldo] bf16.
  * h is bf16(silu_locked(bf16(gate)) * bf16(up)), so the result equals
  * gnf4_hip_nf4_fwd (gate_up) -> gnf4_hip_silu_mul -> gnf4_hip_nf4_fwd (down)
@@ -143,6 +148,13 @@ int gnf4_hip_silu_mul(const void *gu, int64_t ldg, int64_t T, int64_t H, void *h
  * header. -1 on bad arguments. No counterpart in the reference (its fused
  * FFN is CPU-only). */
 int64_t gnf4_hip_ffn_sync_words(int G, int64_t N_gu, int64_t N_dn);
+
+/* Polls a fused-FFN down unit makes before it gives up waiting for h
+ * (default 2^22), for launches after this call. A diagnostics and test
+ * knob: 0 makes every down unit that does not find its h ready at the first
+ * poll write NaN and set the error word. -1 on a negative value. No
+ * counterpart in the reference. */
+int gnf4_hip_ffn_set_spin_limit(int polls);
 
 int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *B_gu,
                          int64_t gu_sbe, int64_t gu_sbn, const float *absmax_gu,

@@ -158,8 +158,7 @@ def test_dgrad_tall_one_hot_rows_are_exact(fmt):
 def test_dgrad_tall_mxfp4_scale_extremes():
     """Small and large e8m0 exponents through the transposed-read kernel: each
     row of a block has its own scale, and one-hot rows give the decoded
-    weights exactly. e8m0 0x00 (2^-127, subnormal results) may come out
-    flushed to zero, as in the forward's e8m0 edge test."""
+    weights exactly, e8m0 0x00 (2^-127, subnormal weights) included."""
     N, K, T = 64, 128, 200
     W, S = rand_mx_stack(1, N, K, seed=15)
     S = S.clone()
@@ -171,10 +170,8 @@ def test_dgrad_tall_mxfp4_scale_extremes():
     go[t, t % N] = 1
     got = _ops()["mxfp4"](go, W, S, [T], [0])
     want = dequant("mxfp4", W[0], S[0]).to(torch.bfloat16)[t % N]
-    sub = torch.zeros_like(want, dtype=torch.bool)
-    sub[:, :32] = (S[0, :, 0] == 0)[t % N].unsqueeze(1)
-    assert torch.equal(got[~sub], want[~sub])
-    assert bool(((got[sub] == want[sub]) | (got[sub] == 0)).all())
+    assert bool((S[0, :, 0] == 0).any())
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])

@@ -256,3 +256,84 @@ def test_many_groups_fused_and_auto_agree():
     auto = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
     assert torch.equal(_bits(fused), _bits(auto))
     assert not nf4_ffn.ffn_sync_error()
+
+
+# ------------------------------------------------------------ sync words --
+
+def test_graph_of_a_smaller_call_survives_a_larger_capture():
+    """Capture a fused call with one group, then one with many groups (it
+    needs a larger sync buffer on the same capture stream), then replay the
+    first graph with eager work in between: its sync words must still be its
+    own (the outgrown buffer is kept alive), so both replays give the
+    composition's bits and no error is raised."""
+    nf4_ffn, nf4_grouped = _mods()
+    H, K, N_dn, E = 256, 512, 384, 64
+    gu_p, gu_a, dn_p, dn_a = _stack(E, H, K, N_dn, seed=60)
+    dev = torch.device("cuda:0")
+    cases = [([1], [5]), ([2, 1, 3, 1] * 12, list(range(0, 48)))]
+    graphs, outs, wants = [], [], []
+    for sizes, ids in cases:
+        a = rand_acts(sum(sizes), K, seed=61 + len(sizes))
+        plan = nf4_grouped.GroupPlan(sizes, ids, dev)
+        wants.append(_composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids))
+        out = torch.empty_like(wants[-1])
+        h = torch.empty(a.shape[0], H, dtype=torch.bfloat16, device=dev)
+        nf4_ffn.launch_ffn_planned(a, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            nf4_ffn.launch_ffn_planned(a, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)
+        graphs.append((g, a, plan, h))
+        outs.append(out)
+    for rep in range(3):
+        for (g, *_), out, want in zip(graphs, outs, wants):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            filler = torch.randn(1 << 20, device=dev)   # eager work between replays
+            del filler
+            assert torch.equal(_bits(out), _bits(want)), rep
+    assert not nf4_ffn.ffn_sync_error()
+
+
+def test_spin_expiry_poisons_the_rows_and_sets_the_error_word():
+    """Force the time-out path from the host (a spin limit of 0 polls: a
+    down unit that does not find its h ready at once gives up) -- every
+    kernel still exits normally. Each down unit's output rows are then
+    either the composition's bits or all NaN, the error word is set exactly
+    when some are NaN, and after clearing it and restoring the limit the
+    next call is exact again (no stale flag passes a later call)."""
+    nf4_ffn, _ = _mods()
+    H, K, N_dn, E = 512, 1024, 1024, 32
+    gu_p, gu_a, dn_p, dn_a = _stack(E, H, K, N_dn, seed=70)
+    sizes, ids = [1, 3, 2, 4, 1, 1, 2, 2], [3, 7, 11, 15, 19, 23, 27, 31]
+    a = rand_acts(sum(sizes), K, seed=71)
+    want = _composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)
+    nf4_ffn.ffn_sync_clear()
+    try:
+        nf4_ffn.set_spin_limit(0)
+        got = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
+        torch.cuda.synchronize()
+    finally:
+        nf4_ffn.set_spin_limit(1 << 22)
+    nan = torch.isnan(got.float())
+    # a down unit covers 32 output columns of one group's rows
+    row0 = 0
+    for m in sizes:
+        for c0 in range(0, N_dn, 32):
+            blk = nan[row0:row0 + m, c0:c0 + 32]
+            assert bool(blk.all()) or not bool(blk.any())
+            if not bool(blk.any()):
+                assert torch.equal(_bits(got[row0:row0 + m, c0:c0 + 32]),
+                                   _bits(want[row0:row0 + m, c0:c0 + 32]))
+        row0 += m
+    timed_out = bool(nan.any())
+    assert nf4_ffn.ffn_sync_error() == timed_out
+    # flags the late gate/up units left behind carry the old call's epoch:
+    # later calls wait for their own, so they are exact without a clear
+    for _ in range(2):
+        again = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
+        assert torch.equal(_bits(again), _bits(want))
+    assert nf4_ffn.ffn_sync_error() == timed_out     # sticky until cleared
+    nf4_ffn.ffn_sync_clear()
+    assert not nf4_ffn.ffn_sync_error()

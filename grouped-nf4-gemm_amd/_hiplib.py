@@ -35,6 +35,9 @@ SIGNATURES = {
     "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
                              _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+    "gnf4_hip_nf4_ffn_fwd_noalloc": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                     _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
+                                     _I64, _I64, _I64, _P, _I64, _P, _I64, _P],
     "gnf4_hip_route_topk": [_P, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64, _P],
     "gnf4_hip_route_groups": [_P, _I64, _I64, _I, _I64, _I, _P, _P, _P, _P, _P, _P],
     "gnf4_hip_route_decode": [_P, _I64, _I64, _I64, _I, _I, _I, _P, _I64, _P, _I64, _P, _I64,

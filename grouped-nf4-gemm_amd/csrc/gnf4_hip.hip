@@ -51,6 +51,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/gnf4_hip.h"
@@ -2878,6 +2879,40 @@ __global__ void __launch_bounds__(256) k_widen_to_bf16(const SrcT* __restrict__ 
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
+// ------------------------------------------------- no-allocation FFN --
+//
+// Sync words of gnf4_hip_nf4_ffn_fwd_noalloc: a fixed device array per GPU
+// (each device that loads this library holds its own copy until the process
+// ends), so that entry point allocates nothing. Zero at load; every call
+// leaves its flags zero again and a flag left behind by a timed-out call
+// carries an older epoch, so nothing has to be cleared between calls. Word 0
+// is the sticky error word (its time-out also writes NaN outputs). Calls
+// that overlap on one GPU share the array and race.
+constexpr int64_t kFfnScratchWords = int64_t(1) << 19;   // 2 MiB
+
+}  // namespace
+
+static __device__ __align__(256) uint32_t scratch[kFfnScratchWords];
+
+namespace {
+
+// Device address of `scratch` per device, resolved once with that device
+// current (the host-side name is not a device address).
+std::mutex g_scratch_mu;
+uint32_t* g_scratch_ptr[64] = {};
+
+uint32_t* ffn_scratch_words() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev] = static_cast<uint32_t*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 // ============================================================== C ABI ====
@@ -3009,6 +3044,24 @@ int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t*
   if (device_cus() <= 0) return -2;
   const FfnSync fs{sync, next_ffn_epoch(), g_ffn_spin_limit.load(std::memory_order_relaxed)};
   return launch_ffn(gu, dn, H, fs, static_cast<hipStream_t>(stream));
+}
+
+int gnf4_hip_nf4_ffn_fwd_noalloc(const void* a, int a_dtype, int64_t lda, const uint8_t* B_gu,
+                                 int64_t gu_sbe, int64_t gu_sbn, const float* absmax_gu,
+                                 int64_t gu_sae, int64_t gu_san, const uint8_t* B_dn,
+                                 int64_t dn_sbe, int64_t dn_sbn, const float* absmax_dn,
+                                 int64_t dn_sae, int64_t dn_san, const int32_t* expert_ids,
+                                 const int32_t* row_off, int G, int max_m, int64_t N_gu,
+                                 int64_t K, int64_t N_dn, void* h, int64_t ldh, void* out,
+                                 int64_t ldo, void* stream) {
+  const int64_t need = gnf4_hip_ffn_sync_words(G, N_gu, N_dn);
+  if (need < 0 || need > kFfnScratchWords) return -1;   // beyond the fixed array
+  uint32_t* words = ffn_scratch_words();
+  if (!words) return -2;
+  return gnf4_hip_nf4_ffn_fwd(a, a_dtype, lda, B_gu, gu_sbe, gu_sbn, absmax_gu, gu_sae, gu_san,
+                              B_dn, dn_sbe, dn_sbn, absmax_dn, dn_sae, dn_san, expert_ids,
+                              row_off, G, max_m, N_gu, K, N_dn, h, ldh, words,
+                              kFfnScratchWords, out, ldo, stream);
 }
 
 int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,

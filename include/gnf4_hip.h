@@ -165,6 +165,26 @@ int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t 
                          int64_t N_dn, void *h, int64_t ldh, uint32_t *sync,
                          int64_t sync_words, void *out, int64_t ldo, void *stream);
 
+/* gnf4_hip_nf4_ffn_fwd without the sync argument, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * sync words live in a fixed per-GPU array of the library (2 MiB, held
+ * until the process ends); the call allocates nothing. Returns -1 when
+ * gnf4_hip_ffn_sync_words(G, N_gu, N_dn) exceeds 524288 words (the
+ * array's size), otherwise what gnf4_hip_nf4_ffn_fwd returns. Every call on
+ * a GPU shares that GPU's array: calls that overlap on one GPU race (run
+ * them in one stream order). A down unit that times out writes NaN into
+ * its output rows; the array's error word is not readable through this
+ * ABI. */
+int gnf4_hip_nf4_ffn_fwd_noalloc(const void *a, int a_dtype, int64_t lda,
+                                 const uint8_t *B_gu, int64_t gu_sbe, int64_t gu_sbn,
+                                 const float *absmax_gu, int64_t gu_sae, int64_t gu_san,
+                                 const uint8_t *B_dn, int64_t dn_sbe, int64_t dn_sbn,
+                                 const float *absmax_dn, int64_t dn_sae, int64_t dn_san,
+                                 const int32_t *expert_ids, const int32_t *row_off, int G,
+                                 int max_m, int64_t N_gu, int64_t K, int64_t N_dn, void *h,
+                                 int64_t ldh, void *out, int64_t ldo, void *stream);
+
 /* Grouped dgrad for either format: out[t, :] = grad_out[t, :] . dequant(W[e(t)]),
  * contracting over N in fixed 64-wide ascending steps (output bits do not
  * depend on block_m). grad_out is [T, ldg] bf16, out is [T, ldo] bf16 with

@@ -82,25 +82,25 @@ DECODE_MAX_ROWS = 16
 
 
 def repack_from_bnb(packed_list, states, N: int, K: int):
-    """bnb per-expert ``quantize_4bit`` output -> ``B [E, N, K//2] u8`` and
-    ``absmax [E, N, K//64] f32`` (reference kernel/nf4_grouped.py:74-96).
-    bnb stores both flat in row-major order, so they reshape when K % 64 == 0;
-    nested (compress_statistics) states are de-nested with bnb itself."""
-    assert K % BLOCKSIZE == 0, f"K={K} not a multiple of blocksize {BLOCKSIZE}"
-    E = len(packed_list)
-    dev = packed_list[0].device
-    B = torch.empty(E, N, K // 2, dtype=torch.uint8, device=dev)
-    A = torch.empty(E, N, K // BLOCKSIZE, dtype=torch.float32, device=dev)
-    for e in range(E):
-        B[e] = packed_list[e].reshape(N, K // 2)
-        st = states[e]
-        am = st.absmax
-        if getattr(st, "nested", False):
-            from bitsandbytes import functional as F
+    """Per-expert bitsandbytes ``quantize_4bit`` results -> the stacked
+    ``B [E, N, K/2]`` uint8 and ``absmax [E, N, K/64]`` fp32 this op takes
+    (reference kernel/nf4_grouped.py:74-96). bitsandbytes keeps both flat and
+    row-major, so with K % 64 == 0 each is a reshape; a nested
+    (compress_statistics) state's absmax is first restored with
+    bitsandbytes' own blockwise dequantize."""
+    if K % BLOCKSIZE:
+        raise AssertionError(f"K={K} is not a multiple of blocksize {BLOCKSIZE}")
 
-            am = F.dequantize_blockwise(st.absmax, st.state2) + st.offset
-        A[e] = am.to(torch.float32).reshape(N, K // BLOCKSIZE)
-    return B, A
+    def absmax_of(state):
+        if not getattr(state, "nested", False):
+            return state.absmax
+        from bitsandbytes import functional as bnb_f
+        return bnb_f.dequantize_blockwise(state.absmax, state.state2) + state.offset
+
+    B = torch.stack([p.reshape(N, K // 2) for p in packed_list])
+    A = torch.stack([absmax_of(st).to(torch.float32).reshape(N, K // BLOCKSIZE)
+                     for st in states])
+    return B.contiguous(), A.contiguous()
 
 
 # ------------------------------------------------------------------ indices --
@@ -773,18 +773,14 @@ def gemm_4bit_grouped(
 
 
 def dequant_ref(packed_row_major: torch.Tensor, absmax: torch.Tensor, N: int, K: int):
-    """Pure-torch reference decode: ``w[n, k] = NF4[code] * absmax[n, k//64]``
-    in fp32, element 2j from the HIGH nibble (reference
-    kernel/nf4_grouped.py:910-929). Runs on any device; it is the checkable
-    decode the error messages point CPU callers to."""
-    lut = _lut(packed_row_major.device)
-    flat = packed_row_major.reshape(-1).to(torch.int32)
-    hi = (flat >> 4) & 0xF
-    lo = flat & 0xF
-    codes = torch.stack([hi, lo], dim=1).reshape(-1)
-    vals = lut[codes]
-    am = absmax.to(torch.float32).reshape(-1).repeat_interleave(BLOCKSIZE)
-    return (vals * am).reshape(N, K)
+    """Plain-torch decode ``w[n, k] = NF4[code(n, k)] * absmax[n, k // 64]``
+    in fp32 (one rounding), element 2j from the high nibble of byte j
+    (reference kernel/nf4_grouped.py:910-929). Runs on any device; it is the
+    checkable decode the CPU refusal points callers to."""
+    b = packed_row_major.reshape(N, K // 2).to(torch.int64)
+    idx = torch.stack((b >> 4, b & 0xF), dim=-1).reshape(N, K // BLOCKSIZE, BLOCKSIZE)
+    scale = absmax.reshape(N, K // BLOCKSIZE, 1).to(torch.float32)
+    return (_lut(packed_row_major.device)[idx] * scale).reshape(N, K)
 
 
 # -------------------------------------------------------------------- dgrad --

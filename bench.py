@@ -98,15 +98,16 @@ def make_mx_layers(E, N, K, layers, dev, seed):
 class DecodeModel:
     """Expert GEMMs of a decode step through every MoE layer."""
 
-    def __init__(self, fmt, cfg, batch, dev, seed=0, layers=None):
+    def __init__(self, fmt, cfg, batch, dev, seed=0, layers=None, weights=None):
         import numpy as np
         import torch
         self.fmt, self.cfg, self.batch, self.dev = fmt, cfg, batch, dev
         L = layers or cfg["layers"]
         E = cfg["E"]
-        mk = make_nf4_layers if fmt == "nf4" else make_mx_layers
-        self.gu = mk(E, *cfg["gu"], L, dev, seed)
-        self.dn = mk(E, *cfg["dn"], L, dev, seed + 1)
+        if weights is None:
+            mk = make_nf4_layers if fmt == "nf4" else make_mx_layers
+            weights = (mk(E, *cfg["gu"], L, dev, seed), mk(E, *cfg["dn"], L, dev, seed + 1))
+        self.gu, self.dn = weights[0][:L], weights[1][:L]
         rng = np.random.default_rng(seed + 7)
         self.routes = []
         g = torch.Generator(device=dev).manual_seed(seed + 3)
@@ -145,6 +146,24 @@ class DecodeModel:
             from nf4_grouped import GroupPlan
             self._plans = [GroupPlan(r[0], r[1], self.dev) for r in self.routes]
         return self._plans
+
+    def eager_us(self, reps=50):
+        """Wall time (us) of one op call as a Python caller sees it (host
+        planning, the group-table upload and the launch; the reference's
+        timing includes the same, bench/phase1/harness.py:915-931): the
+        gate_up op of layer 0 called back to back, averaged."""
+        import torch
+        op = self.op()
+        sizes, eids, x, h = self.routes[0]
+        ids = eids.cpu().tolist()
+        for _ in range(5):
+            op(x, *self.gu[0], sizes, ids)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            op(x, *self.gu[0], sizes, ids)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e6 / reps
 
     def kernel_ms(self, which="gu", replays=20):
         """Average duration (ms) of one projection's kernel: every layer's
@@ -264,6 +283,20 @@ def ffn_report(model):
     return r
 
 
+def decode_report(m):
+    """Per-launch rates of one decode configuration: gate_up and down packed
+    GB/s (graph of every layer's launches, HIP events), active experts per
+    layer, and the eager per-call wall time of the op."""
+    gu = m.kernel_ms("gu")
+    dn = m.kernel_ms("dn")
+    return {"gate_up_us": round(gu * 1e3, 3),
+            "gate_up_gbs": round(sum(m.bytes_gu) / m.L / (gu * 1e-3) / 1e9, 1),
+            "down_us": round(dn * 1e3, 3),
+            "down_gbs": round(sum(m.bytes_dn) / m.L / (dn * 1e-3) / 1e9, 1),
+            "experts_per_layer": round(sum(len(r[0]) for r in m.routes) / m.L, 1),
+            "eager_op_us": round(m.eager_us(), 2)}
+
+
 def time_graph(fn, steps, warmup, dev, settle=False):
     """Capture fn() as a graph, then time `steps` replays after `warmup`
     (and, with `settle`, after further replays filling 30 ms)."""
@@ -297,47 +330,36 @@ def time_graph(fn, steps, warmup, dev, settle=False):
     return (time.perf_counter() - t0) * 1e3 / steps, graph
 
 
-def cpu_baseline(model, budget_s=10.0, layers=4):
-    """The reference's CPU kernels on the host cores over a bounded sample:
-    `layers` layers of the same decode workload (gate_up + down per layer),
-    repeated until ~budget_s of CPU time. fp32 activations are converted
-    once, outside the timed region (as the reference's CPU tier does)."""
-    import numpy as np
-    from oracle import native
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
-    ref = native.ref_lib()
-    kind = "reference" if ref is not None else "port"
-    fwd = native.ref_gemv_grouped if ref is not None else native.gemv_grouped
-    L = min(layers, model.L)
-    host = []
-    for l in range(L):
-        sizes, eids, x, h = model.routes[l]
-        ids = eids.cpu().tolist()
-        host.append((sizes, ids, x.float().cpu().numpy(), h.float().cpu().numpy(),
-                     model.gu[l][0].cpu().numpy(), model.gu[l][1].cpu().numpy(),
-                     model.dn[l][0].cpu().numpy(), model.dn[l][1].cpu().numpy()))
-    nbytes = sum(model.bytes_gu[:L]) + sum(model.bytes_dn[:L])
-    fmt = model.fmt
-
-    def one_pass():
-        for sizes, ids, x, h, gw, gs, dw, ds in host:
-            fwd(x, gw, gs, sizes, ids, fmt=fmt, threads=threads)
-            fwd(h, dw, ds, sizes, ids, fmt=fmt, threads=threads)
-
-    one_pass()                                       # warm the pages
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        one_pass()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    gbs = nbytes * reps / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{reps} passes x {L} layers (gate_up+down, batch {model.batch}, "
-                      f"top-{model.cfg['top_k']}) in {el:.1f} s; "
-                      f"{'oracle/_ref ' + native.ref_path().name if ref is not None else 'oracle/liboracle.so'}",
-            "ms_per_layer_pass": round(el * 1e3 / reps / L, 3)}
+def cpu_baseline(layers, seconds=8.0):
+    """The reference's CPU kernels (oracle/_ref, compiled from
+    gnf4_native/cpu_kernels.c; the C restatement where that build is absent)
+    on the same decode workload, run by ``python -m oracle.cpu_baseline`` as
+    a child process under the reference's pinning contract
+    (OMP_PLACES=cores OMP_PROC_BIND=spread, gnf4_native/cpu_kernels.c:47-51),
+    at all physical cores of this process's CPU set and at one thread; the
+    median of >= 10 timed passes over every layer's own weight bytes."""
+    import subprocess
+    env = dict(os.environ, OMP_PLACES="cores", OMP_PROC_BIND="spread")
+    cmd = [sys.executable, "-m", "oracle.cpu_baseline", "--layers", str(layers),
+           "--seconds", str(seconds)]
+    r = subprocess.run(cmd, cwd=str(ROOT), env=env, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        log(f"[bench] cpu baseline failed: {r.stderr[-2000:]}")
+        return None
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    allc, one = res["all_cores"], res["one_thread"]
+    model = res["lscpu"].get("Model name", "?")
+    return {"value": allc["gbs"], "unit": "GB/s", "cores": allc["threads"], "kind": res["kind"],
+            "sample": f"median of {allc['runs']} passes over {res['layers']} layers' own weights "
+                      f"(gate_up 8x1536x2048 + down 8x2048x768 NF4 GEMV per layer, batch 1, "
+                      f"{res['packed_bytes_per_pass'] / 1e6:.0f} MB packed per pass), "
+                      f"{allc['threads']} threads = every physical core of the process's CPU set "
+                      f"({res['affinity_cpus']} CPUs), OMP_PLACES=cores OMP_PROC_BIND=spread; "
+                      f"{model}",
+            "median_ms_per_pass": allc["median_ms"],
+            "one_thread": {"value": one["gbs"], "median_ms_per_pass": one["median_ms"],
+                           "runs": one["runs"]},
+            "lscpu": res["lscpu"], "library": res["library"]}
 
 
 def _timed(fn, dev, reps=10):
@@ -467,7 +489,7 @@ def main():
     ap.add_argument("--layers", type=int, default=QWEN["layers"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--mma-workload", action="store_true",
                     help="for rocprofv3: the prefill (config 4) and dgrad (config 5) "
                          "measurements only")
@@ -514,21 +536,27 @@ def main():
     extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1)}}
     extra[f"qwen3_nf4_ffn_b{args.batch}"] = ffn_report(model)
     log(f"[bench] ffn: {json.dumps(extra[f'qwen3_nf4_ffn_b{args.batch}'])}")
+    extra["qwen3_nf4_decode_b1_eager_op_us"] = round(model.eager_us(), 2)
     if not args.no_extra:
-        for b in (4, 16):
-            m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=8)
-            a = sum(m.bytes_gu) / len(m.bytes_gu) / (m.kernel_ms("gu") * 1e-3) / 1e9
-            a2 = sum(m.bytes_dn) / len(m.bytes_dn) / (m.kernel_ms("dn") * 1e-3) / 1e9
-            extra[f"qwen3_nf4_decode_b{b}"] = {"gate_up_gbs": round(a, 1), "down_gbs": round(a2, 1),
-                                               "experts_per_layer": round(sum(len(r[0]) for r in m.routes) / m.L, 1)}
-            extra[f"qwen3_nf4_ffn_b{b}"] = ffn_report(m)
+        # config 2's batch sweep on 16 of the model's layers (their own bytes)
+        sweep = {}
+        for b in (1, 4, 16):
+            m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=16, weights=(model.gu, model.dn))
+            sweep[f"b{b}"] = decode_report(m)
+            if b > 1:
+                extra[f"qwen3_nf4_ffn_b{b}"] = ffn_report(m)
             del m
-        for b in (1, 64):
-            m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=6)
-            a = sum(m.bytes_gu) / len(m.bytes_gu) / (m.kernel_ms("gu") * 1e-3) / 1e9
-            a2 = sum(m.bytes_dn) / len(m.bytes_dn) / (m.kernel_ms("dn") * 1e-3) / 1e9
-            extra[f"gptoss20b_mxfp4_decode_b{b}"] = {"gate_up_gbs": round(a, 1), "down_gbs": round(a2, 1)}
+        extra["qwen3_nf4_decode_sweep"] = sweep
+        # config 3's batch sweep, GPT-OSS-20B MXFP4 experts (6 layers' own bytes)
+        mx = (make_mx_layers(GPTOSS["E"], *GPTOSS["gu"], 6, dev, 100),
+              make_mx_layers(GPTOSS["E"], *GPTOSS["dn"], 6, dev, 101))
+        sweep = {}
+        for b in (1, 2, 4, 8, 16, 32, 64):
+            m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=6, weights=mx)
+            sweep[f"b{b}"] = decode_report(m)
             del m
+        extra["gptoss20b_mxfp4_decode_sweep"] = sweep
+        del mx
         torch.cuda.empty_cache()
         extra["qwen3_nf4_prefill_zipf"] = prefill_tflops(dev)
         extra["qwen3_nf4_dgrad_down"] = dgrad_tflops(dev)
@@ -537,7 +565,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("[bench] timing the CPU baseline")
-        cpu = cpu_baseline(model, budget_s=args.cpu_seconds)
+        cpu = cpu_baseline(model.L, seconds=args.cpu_seconds)
         log(f"[bench] cpu: {cpu}")
 
     line = {

@@ -1454,6 +1454,9 @@ __global__ void __launch_bounds__(512, 2)
     while (StepUnroll<0, kS>::run(st)) {
     }
   }
+  // the past-the-end direct-to-LDS loads (zero-size resources) still write
+  // their LDS slots: let them land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // 256-row tiles (k_prefill_w below).
@@ -1942,8 +1945,11 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   // ---- epilogue: the bf16 tile goes through LDS (free now: every wave is
   // past its last operand read), so the global stores write whole rows.
   // LDS tile: row r at r * 512 bytes, 16-byte chunk c at (c ^ (r % 32)) * 16.
+  // Every load must have landed first, the past-the-end ones included: a
+  // direct-to-LDS load through a zero-size resource still writes (zeros) to
+  // its LDS slot, which the tile below overlaps.
   __builtin_amdgcn_sched_barrier(0);
-  wait_vm_lgkm0<63>();
+  wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
   if constexpr (DG) {
     // MFMA row 8 g + 4 h + q of block b is column 64 w + 2 (8 g + 4 h + q) + b:
@@ -2310,6 +2316,9 @@ __global__ void __launch_bounds__(512, 2)
     while (StepUnroll<0, kS>::run(st)) {
     }
   }
+  // the past-the-end direct-to-LDS loads (zero-size resources) still write
+  // their LDS slots: let them land before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // ================================================================= dgrad ==

@@ -815,6 +815,266 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
       q, g, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, 0u, NoWait{});
 }
 
+// ------------------------------------------------- row-streaming decode --
+//
+// k_decode_rows<FMT, kW, kT, kSets, kCpw, kR, kP>: decode (every group <= 16
+// rows) for launches with many groups (batched decode). Each wave owns
+// 16 kT weight rows of one group over the whole K, so no partial sums cross
+// waves: the wave streams its rows' 128-element chunks through a register
+// ring of kD = kCpw * kR chunks of loads in flight (16 bytes of packed
+// weights per lane and tile; NF4 absmax once per chunk pair, 16 bytes),
+// decodes and multiplies each chunk as it lands, and refills the slot with
+// the chunk kD ahead. The ring loop is straight-line code (chunks past the
+// end load zeros and add nothing), so the loads stay in flight across
+// iterations. A workgroup of kW waves covers 16 kT kW rows of one group:
+// its activation rows (at most kP 16-byte pieces per thread) are staged
+// once into LDS, next to the NF4 split table, while the first chunks are in
+// flight. Staged layout: piece (k / 8, row m) at ((k / 8) M + m + k / 32)
+// x 16 bytes -- the extra 16 bytes per 32 elements put the four quarters of
+// a wave's operand reads on different banks -- then a zero block.
+// Bits: the MFMA row semantics and operands are those of decode_unit (NF4:
+// rows 0-7 and 8-15 hold the two absmax blocks of a chunk for tokens
+// 8 s + 0..7; MXFP4: 16 token rows), and the wave folds its chunk sums in
+// decode_unit's order: chunks in runs of kCpw (the run wave w of a
+// k_decode_fwd launch takes when the launch needs one round), each run
+// summed in its own chain, the runs added in order. So both kernels -- and
+// the fused FFN, which runs decode_unit -- give identical outputs.
+template <int FMT, int kW, int kT, int kSets, int kCpw, int kR, int kP>
+__global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr bool kSplit = FMT == kNF4;
+  static_assert(kSets == 1 || (kSplit && kSets == 2), "row sets");
+  constexpr int kD = kCpw * kR;
+  static_assert(!kSplit || kD % 2 == 0, "NF4 absmax comes per chunk pair");
+  constexpr int kScaleBytes = FMT == kNF4 ? 4 : 1;
+  const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
+  __builtin_amdgcn_sched_barrier(0);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;
+  const int q = lane >> 4;
+  const int g = (int)blockIdx.y;
+
+  const int32_t* ce = p.eids + g;
+  const int32_t* cr = p.row_off ? p.row_off + g : ce;
+  const int32_t* cr1 = p.row_off ? cr + 1 : ce;
+  const int one = p.row_off ? 1 : 0;
+  int e32, ro_a, ro_b;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(ce), "s"(cr), "s"(cr1)
+      : "memory");
+  const int64_t e = e32;
+  const int r0 = one ? ro_a : g;
+  const int M = one ? ro_b - ro_a : 1;
+  if (M <= 0) return;  // uniform across the workgroup (empty group)
+  const int K32 = (int)p.K;
+  const int nchunks = (K32 + 127) >> 7;
+
+  // ---- activation staging loads first: they are waited on first
+  const int a_base = FMT == kNF4 ? kSplitTabBytes : 0;
+  const int kslices = K32 >> 3;
+  const int pieces = M * kslices;
+  const int zero_off = a_base + (pieces + (kslices >> 2) + 1) * 16;
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
+  u32x4_t av[kP];
+#pragma unroll
+  for (int j = 0; j < kP; ++j) {
+    const int pc = j * 64 * kW + (int)threadIdx.x;
+    const int m = pc / kslices, sl = pc - m * kslices;
+    av[j] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+  }
+
+  // ---- the ring's first kD chunks
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(
+      static_cast<const char*>(p.S) + e * p.sse * kScaleBytes, p.N * p.ssn * kScaleBytes);
+  int64_t n[kT];
+  int b_row[kT], s_row[kT];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) {
+    n[t] = (int64_t)blockIdx.x * (16 * kW * kT) + (wave * kT + t) * 16 + nl;
+    b_row[t] = n[t] < p.N ? (int)(n[t] * p.sbn) + q * 16 : kOOB;
+    // NF4: the row's absmax (blocks 4 h .. 4 h + 3 of chunk pair h); MXFP4:
+    // the lane's scale byte (block 4 c + q)
+    s_row[t] = n[t] < p.N ? (int)(n[t] * p.ssn * kScaleBytes) + (FMT == kNF4 ? 0 : q) : kOOB;
+  }
+  u32x4_t wr[kD][kT];
+  u32x4_t sq[kSplit ? kD / 2 : 1][kT];   // NF4 absmax of chunk pairs
+  unsigned sb[kSplit ? 1 : kD][kT];      // MXFP4 scale bytes
+  auto issue = [&](int c, int slot) {
+    // past the end of K (the second half of a last 64-element chunk, or the
+    // ring's refills beyond the last chunk): zeros
+    const bool ok = (unsigned)(c * 128 + q * 32) < (unsigned)K32;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      wr[slot][t] = buf_load16(rb, oob_unless(ok, b_row[t] + c * 64));
+      if constexpr (kSplit) {
+        if ((slot & 1) == 0)
+          sq[slot / 2][t] = buf_load16(rs, oob_unless((unsigned)(c * 128) < (unsigned)K32,
+                                                      s_row[t] + c * 8));
+      } else {
+        sb[slot][t] = buf_load1(rs, oob_unless(ok, s_row[t] + c * 4));
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kD; ++i) issue(i, i);
+
+  // ---- LDS: [NF4 split table][activations M x K, padded][zero block]
+#pragma unroll
+  for (int j = 0; j < kP; ++j) {
+    const int pc = j * 64 * kW + (int)threadIdx.x;
+    if (pc < pieces) {
+      const int m = pc / kslices, sl = pc - m * kslices;
+      *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m + (sl >> 2)) * 16) = av[j];
+    }
+  }
+  if (threadIdx.x < 4)
+    *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
+  if constexpr (FMT == kNF4) init_split_table(smem, lut);
+  __syncthreads();
+
+  // NF4: A row nl carries token (nl & 7) + 8 s in the quarters of block
+  // nl / 8 only; MXFP4: token nl
+  const bool blk_lane = !kSplit || ((nl < 8) == (q < 2));
+  const int tok = kSplit ? (nl & 7) : nl;
+  const unsigned lane_off = (unsigned)(uintptr_t)smem | (unsigned)(lane & (kSplitCols - 1)) * 16u;
+  // per row set: the lane's activation row offset (or -1)
+  int a_row[kSets];
+#pragma unroll
+  for (int s = 0; s < kSets; ++s)
+    a_row[s] = (blk_lane && tok + 8 * s < M) ? a_base + (tok + 8 * s) * 16 : -1;
+  // acc: the current run's chains (NF4: [t][s][0]; MXFP4: alternate
+  // k-slices); tot: the runs folded so far (it starts at +0, which a first
+  // run adds to exactly: no run sum is -0)
+  f32x4_t acc[kT][kSets][2], tot[kT][kSets];
+#pragma unroll
+  for (int t = 0; t < kT; ++t)
+#pragma unroll
+    for (int s = 0; s < kSets; ++s)
+      acc[t][s][0] = acc[t][s][1] = tot[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int c, const u32x4_t (&w)[kT], const float (&scl)[kT]) {
+    const int kp = c * 16 + q * 4;   // first 16-byte activation piece of the lane's slice
+    const bool kval = kp < kslices;
+    u32x4_t a[kSets][4];
+#pragma unroll
+    for (int s = 0; s < kSets; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int off = (kval && a_row[s] >= 0)
+                            ? a_row[s] + ((kp + j) * M + ((kp + j) >> 2)) * 16 : zero_off;
+        a[s][j] = *reinterpret_cast<const u32x4_t*>(smem + off);
+      }
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      if constexpr (kSplit) {
+        f32x4_t cs[kSets][2];
+#pragma unroll
+        for (int s = 0; s < kSets; ++s) cs[s][0] = cs[s][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x4_t d[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            d[b] = lds_read16(
+                __builtin_amdgcn_perm(w[t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
+          const u32x4_t hi = {d[0][0], d[1][0], d[2][0], d[3][0]};
+          const u32x4_t mid = {d[0][1], d[1][1], d[2][1], d[3][1]};
+          const u32x4_t lo = {d[0][2], d[1][2], d[2][2], d[3][2]};
+#pragma unroll
+          for (int s = 0; s < kSets; ++s) {
+            cs[s][j & 1] = mfma(a[s][j], hi, cs[s][j & 1]);
+            cs[s][j & 1] = mfma(a[s][j], mid, cs[s][j & 1]);
+            cs[s][j & 1] = mfma(a[s][j], lo, cs[s][j & 1]);
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < kSets; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[t][s][0][r] = __builtin_fmaf(cs[s][0][r] + cs[s][1][r], scl[t], acc[t][s][0][r]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[t][0][j & 1] = mfma(a[0][j], mx_dword_to_bf16(w[t][j], scl[t]), acc[t][0][j & 1]);
+      }
+    }
+  };
+  auto fold = [&]() {
+#pragma unroll
+    for (int t = 0; t < kT; ++t)
+#pragma unroll
+      for (int s = 0; s < kSets; ++s) {
+        f32x4_t v;
+        if constexpr (kSplit) {
+          // lanes 0..31 take their second block's rows from lane + 32
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = acc[t][s][0][r] + __shfl_xor(acc[t][s][0][r], 32);
+        } else {
+          v = acc[t][s][0] + acc[t][s][1];
+        }
+        tot[t][s] = tot[t][s] + v;
+        acc[t][s][0] = acc[t][s][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+
+  u32x4_t pair_sq[kT];   // NF4: the current chunk pair's absmax (taken before its refill)
+  for (int c0 = 0; c0 < nchunks; c0 += kD) {
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+#pragma unroll
+      for (int i = 0; i < kCpw; ++i) {
+        const int slot = r * kCpw + i;
+        const int c = c0 + slot;
+        u32x4_t w[kT];
+        float scl[kT];
+        const bool kval = (unsigned)(c * 128 + q * 32) < (unsigned)K32;
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          w[t] = wr[slot][t];
+          if constexpr (kSplit) {
+            // absmax block 2 c + q / 2: element 2 (c % 2) + q / 2 of the pair's
+            // four; a lane past the end of K multiplies zeros by zero
+            if ((slot & 1) == 0) pair_sq[t] = sq[slot / 2][t];
+            const u32x4_t v = pair_sq[t];
+            const unsigned lo2 = (slot & 1) ? v[2] : v[0], hi2 = (slot & 1) ? v[3] : v[1];
+            scl[t] = kval ? __uint_as_float(q >= 2 ? hi2 : lo2) : 0.f;
+          } else {
+            scl[t] = e8m0_to_f32(sb[slot][t]);
+          }
+        }
+        issue(c + kD, slot);
+        compute(c, w, scl);
+        __builtin_amdgcn_sched_barrier(0);   // one chunk's registers at a time
+      }
+      fold();
+    }
+  }
+
+  // ---- outputs
+#pragma unroll
+  for (int t = 0; t < kT; ++t)
+#pragma unroll
+    for (int s = 0; s < kSets; ++s) {
+      const f32x4_t v = tot[t][s];
+      if ((!kSplit || q < 2) && n[t] < p.N) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = (kSplit ? 8 * s : 0) + 4 * q + i;
+          if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n[t]] = f32_to_bf16_bits(v[i]);
+        }
+      }
+    }
+  // the ring's last refills (past the end: zero-size offsets) are in flight
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 // ------------------------------------------------------------ fused FFN --
 //
 // gate_up -> silu(gate) * up -> down for groups of at most 16 rows, in one
@@ -2591,12 +2851,92 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   }
 }
 
+// Chunks per wave of a k_decode_fwd launch (its rounds' length).
+template <int FMT>
+int decode_cpw(int64_t K, int64_t max_m) {
+  constexpr int kW = 8;
+  const int64_t per_wave = ((K + 127) / 128 + kW - 1) / kW;
+  const bool stage = max_m <= 2 && max_m * K * 2 <= 4 * 64 * kW * 16;
+  if (per_wave <= 1) return 1;
+  if (FMT == kNF4 || per_wave <= 2) return 2;
+  if (per_wave <= 3 || !stage) return 3;
+  return 4;
+}
+
+// Row-streaming decode (k_decode_rows) for a launch whose k_decode_fwd
+// form needs one round per wave (so the two kernels' bits agree); returns 1
+// when this launch is not for it.
+template <int FMT, int W, int T, int S, int CPW, int R, int P>
+int launch_rows_inst(const FwdArgs& p, int lds, hipStream_t stream) {
+  static int configured_dev = -1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  if (configured_dev != dev) {
+    if (hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&k_decode_rows<FMT, W, T, S, CPW, R, P>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return -2;
+    configured_dev = dev;
+  }
+  const dim3 grid((unsigned)((p.N + 16 * W * T - 1) / (16 * W * T)), (unsigned)p.G, 1);
+  hipLaunchKernelGGL((k_decode_rows<FMT, W, T, S, CPW, R, P>), grid, dim3(64 * W), lds, stream,
+                     p);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// ring: kCpw x kR chunks per wave
+template <int FMT, int W, int S, int P>
+int launch_rows_cpw(const FwdArgs& p, int cpw, int lds, hipStream_t stream) {
+  // (fewer than 8 chunks: k_decode_fwd runs one chunk per wave)
+  if (cpw != 1) return 1;
+  return launch_rows_inst<FMT, W, 2, S, 1, 2, P>(p, lds, stream);
+}
+
+// Taken for NF4 launches of groups of 2..8 rows whose K gives k_decode_fwd's
+// eight waves fewer than eight chunks (K <= 768: idle waves there). Measured
+// on MI355X, Qwen3-30B-A3B down projection (K = 768): batch 4 1241 -> 1721
+// GB/s, batch 16 1405 -> 2267 GB/s; at K = 2048 and for MXFP4 (K = 2880)
+// the split-K kernel stays faster, and two row sets spill here.
+template <int FMT>
+int launch_rows(const FwdArgs& p, hipStream_t stream) {
+  if constexpr (FMT != kNF4) {
+    return 1;
+  } else {
+  if (p.max_m < 2 || p.max_m > 8 || p.G <= 0 || p.G > 65535) return 1;
+  const int64_t nchunks = (p.K + 127) / 128;
+  if (nchunks >= 8) return 1;
+  const int cpw = decode_cpw<FMT>(p.K, p.max_m);
+  if (nchunks > 8 * cpw) return 1;                     // k_decode_fwd takes rounds
+  const int64_t kslices = p.K / 8;
+  const int64_t pieces = (int64_t)p.max_m * kslices;
+  const int64_t lds = (FMT == kNF4 ? kSplitTabBytes : 0) + (pieces + kslices / 4 + 1) * 16 + 64;
+  if (lds > 160 * 1024) return 1;
+  const int sets = FMT == kNF4 && p.max_m > 8 ? 2 : 1;
+  const bool two = lds <= 80 * 1024;                  // two workgroups of 8 waves per CU
+  const int64_t threads = two ? 512 : 1024;
+  const int pp = (int)((pieces + threads - 1) / threads);
+  if (pp > 8) return 1;
+  const int P = pp <= 2 ? 2 : pp <= 4 ? 4 : 8;
+  (void)sets;
+  if (two) return P == 2 ? launch_rows_cpw<FMT, 8, 1, 2>(p, cpw, (int)lds, stream)
+                 : P == 4 ? launch_rows_cpw<FMT, 8, 1, 4>(p, cpw, (int)lds, stream)
+                          : launch_rows_cpw<FMT, 8, 1, 8>(p, cpw, (int)lds, stream);
+  return P == 2 ? launch_rows_cpw<FMT, 16, 1, 2>(p, cpw, (int)lds, stream)
+         : P == 4 ? launch_rows_cpw<FMT, 16, 1, 4>(p, cpw, (int)lds, stream)
+                  : launch_rows_cpw<FMT, 16, 1, 8>(p, cpw, (int)lds, stream);
+  }
+}
+
 // Unit height: 32 rows, or 16 for single-row MXFP4 groups (more workgroups
 // for a stream that needs little decode work per byte).
 // Groups go to the grid's rows, at most 65535 per launch: larger calls run as
 // several launches over consecutive group ranges.
 template <int FMT>
 int launch_decode(const FwdArgs& p, hipStream_t stream) {
+  {
+    const int rc = launch_rows<FMT>(p, stream);
+    if (rc <= 0) return rc;
+  }
   for (int g0 = 0; g0 < p.G; g0 += 65535) {
     FwdArgs q = p;
     q.G = p.G - g0 < 65535 ? p.G - g0 : 65535;

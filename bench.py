@@ -421,7 +421,8 @@ def pmc_workload(model):
     """Kernels for the HBM-traffic counter passes: a plain device copy of
     exactly 256 MiB (reads 256 MiB, writes 256 MiB) whose FETCH_SIZE /
     WRITE_SIZE readings give the scale factor, then every layer's gate_up
-    decode launch (cold weights: each layer is its own 302 MB buffer)."""
+    decode launch (cold weights: each layer is its own buffer), twice, then
+    every layer's down launch, twice."""
     import torch
     from nf4_grouped import launch_planned
     src = torch.empty(256 << 20, dtype=torch.uint8, device=model.dev).fill_(1)
@@ -430,19 +431,24 @@ def pmc_workload(model):
     dst.copy_(src)
     torch.cuda.synchronize()
     plans = model.plans()
-    for _ in range(2):
-        for l in range(model.L):
-            sizes, eids, x, h = model.routes[l]
-            launch_planned(0, x, *model.gu[l], plans[l])
-        torch.cuda.synchronize()
-    log(f"[bench] pmc workload: 1 copy of {src.numel()} B, {2 * model.L} gate_up launches "
-        f"of {model.bytes_gu[0]} packed B")
+    fmt = 0 if model.fmt == "nf4" else 1
+    for which in ("gu", "dn"):
+        for _ in range(2):
+            for l in range(model.L):
+                sizes, eids, x, h = model.routes[l]
+                a, (W, S) = (x, model.gu[l]) if which == "gu" else (h, model.dn[l])
+                launch_planned(fmt, a, W, S, plans[l])
+            torch.cuda.synchronize()
+    log(f"[bench] pmc workload ({model.fmt}, batch {model.batch}): 1 copy of {src.numel()} B, "
+        f"{2 * model.L} gate_up launches (mean {sum(model.bytes_gu) / model.L:.0f} packed B), "
+        f"then {2 * model.L} down launches (mean {sum(model.bytes_dn) / model.L:.0f} packed B)")
 
 
 def pmc_prefill_workload(dev, seed=0):
     """Kernels for the prefill HBM-traffic counter passes: the 256 MiB copy
     (calibration), then config 4's gate_up and down calls (Zipf routing,
-    32768 rows), each three times, eagerly."""
+    32768 rows), each three times, then config 5's dgrad (16384 rows), three
+    times, eagerly."""
     import numpy as np
     import torch
     from nf4_grouped import gemm_4bit_grouped
@@ -462,6 +468,13 @@ def pmc_prefill_workload(dev, seed=0):
         for _ in range(3):
             gemm_4bit_grouped(a, Wt, At, sizes, eids)
         torch.cuda.synchronize()
+    from nf4_grouped import dgrad_4bit_grouped
+    d_sizes, d_ids = route(np.random.default_rng(seed + 1), 2048, 8, 128)
+    go = (torch.randn(sum(d_sizes), 2048, device=dev) * 1e-2).to(torch.bfloat16)
+    d_eids = torch.tensor(d_ids, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        dgrad_4bit_grouped(go, W2, A2, d_sizes, d_eids)
+    torch.cuda.synchronize()
     log(f"[bench] pmc prefill workload: 1 copy of {src.numel()} B, 3 gate_up + 3 down calls, {T} rows")
 
 
@@ -497,6 +510,8 @@ def main():
                     help="for rocprofv3 --pmc: one 256 MiB device copy (the counter "
                          "calibration), then the gate_up decode kernel of every layer, "
                          "launched eagerly twice; prints nothing else")
+    ap.add_argument("--fmt", choices=("nf4", "mxfp4"), default="nf4",
+                    help="with --pmc-workload: Qwen3 NF4 (default) or GPT-OSS-20B MXFP4 experts")
     ap.add_argument("--pmc-prefill-workload", action="store_true",
                     help="for rocprofv3 --pmc: the 256 MiB copy, then config 4's prefill "
                          "gate_up and down calls, three each")
@@ -517,6 +532,9 @@ def main():
         log(f"[bench] dgrad {json.dumps(dgrad_tflops(dev))}")
         return
     log(f"[bench] building Qwen3-30B-A3B NF4 decode model: {args.layers} layers, batch {args.batch}")
+    if args.pmc_workload and args.fmt == "mxfp4":
+        pmc_workload(DecodeModel("mxfp4", GPTOSS, args.batch, dev, layers=min(args.layers, 8)))
+        return
     model = DecodeModel("nf4", QWEN, args.batch, dev, layers=args.layers)
     if args.pmc_workload:
         pmc_workload(model)

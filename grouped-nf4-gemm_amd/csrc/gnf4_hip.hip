@@ -1772,8 +1772,8 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_t16(const char* lds0, unsig
 // (workgroups per XCD)-th tile of it; the NF4 pair table is built once per
 // workgroup.
 // The k order of every output element is that of k_prefill, so both give
-// identical bits. Tiles of at most 128 or 64 rows skip the
-// MFMAs and operand reads of their empty 32-row subtiles.
+// identical bits. A tile runs MFMAs and operand reads for its own 32-row
+// subtiles only (one instantiation per count, 2..8).
 //
 // LDS map: activation stages at 0, 32 and 64 KiB; weight ring at 96 KiB
 // (three 10 KiB slots: 8 KiB of packed bytes, then the scales); the 16-column
@@ -2161,11 +2161,11 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       using QN = std::integral_constant<int, qn>;
       using QC = std::integral_constant<int, qc>;
       using DT = std::integral_constant<int, (kk + 3) & 3>;
-      constexpr int kPer = 8 / kM;
       // per 32-row subtile i: its two MFMAs, the reload of its operand for
-      // the next slice, and 8 / kM pieces of the lookup (next target) and of
-      // the math (this slice's target), fenced so that the decode work sits
-      // between MFMAs and runs while they execute
+      // the next slice, and its share (pieces 8 i / kM .. 8 (i + 1) / kM) of
+      // the lookup (next target) and of the math (this slice's target),
+      // fenced so that the decode work sits between MFMAs and runs while
+      // they execute
 #pragma unroll
       for (int i = 0; i < kM; ++i) {
 #pragma unroll
@@ -2189,7 +2189,7 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
           if constexpr (kk == 3) issue_a(f + 3, j, j + 1);
         }
 #pragma unroll
-        for (int pc = i * kPer; pc < (i + 1) * kPer; ++pc) {
+        for (int pc = (8 * i) / kM; pc < (8 * (i + 1)) / kM; ++pc) {
           lookup_pc(QN{}, x0, x1, xs, f + 1, kk, pc);
           math_pc(QC{}, DT{}, pc);
         }
@@ -2288,12 +2288,16 @@ __global__ void __launch_bounds__(256, 1)
     t.row0 = t_row0[mt];
     t.rows = t_rows[mt];
     t.e = eids[t_group[mt]];
-    if (t.rows > 128)
-      prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut, first);
-    else if (t.rows > 64)
-      prefill_w_tile<FMT, 4, DG>(p, t, smem, out, lut, first);
-    else
-      prefill_w_tile<FMT, 2, DG>(p, t, smem, out, lut, first);
+    // MFMAs for the tile's 32-row subtiles only
+    switch ((t.rows + 31) >> 5) {
+      case 8: prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut, first); break;
+      case 7: prefill_w_tile<FMT, 7, DG>(p, t, smem, out, lut, first); break;
+      case 6: prefill_w_tile<FMT, 6, DG>(p, t, smem, out, lut, first); break;
+      case 5: prefill_w_tile<FMT, 5, DG>(p, t, smem, out, lut, first); break;
+      case 4: prefill_w_tile<FMT, 4, DG>(p, t, smem, out, lut, first); break;
+      case 3: prefill_w_tile<FMT, 3, DG>(p, t, smem, out, lut, first); break;
+      default: prefill_w_tile<FMT, 2, DG>(p, t, smem, out, lut, first); break;
+    }
     first = false;
   }
 }

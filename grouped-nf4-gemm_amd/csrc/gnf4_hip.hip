@@ -481,7 +481,10 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   const int kslices = K32 >> 3;                       // 16-byte activation pieces per row
   int* const s_status = reinterpret_cast<int*>(smem + (FMT == kNF4 ? kSplitTabBytes : 0));
   const int a_base = (FMT == kNF4 ? kSplitTabBytes : 0) + kDecodeFlagBytes;
-  const int zero_off = a_base + ((M * kslices * 16 + 15) & ~15);
+  // staged piece (k / 8, row m) at ((k / 8) M + m + k / 32) x 16 bytes: the
+  // extra 16 bytes per 32 elements put the four quarters of a wave's operand
+  // reads on different banks
+  const int zero_off = a_base + (M * kslices + (kslices >> 2) + 1) * 16;
 
   // ---- activation staging loads (first in the queue: they are waited on first)
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
@@ -596,7 +599,7 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
         const int pc = (int)threadIdx.x + i * kThreadsD;
         if (wave * 64 + i * kThreadsD < pieces && pc < pieces) {
           const int m = pc / kslices, sl = pc - m * kslices;
-          *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m) * 16) = av[i];
+          *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m + (sl >> 2)) * 16) = av[i];
         }
       }
       __syncthreads();
@@ -609,14 +612,17 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
       if constexpr (kOneRow) {
         // every lane: the group's one row over its 32 elements
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
+          const int sl = (int)(kseg >> 3) + j;
           a[0][j] = *reinterpret_cast<const u32x4_t*>(
-              smem + (kval ? a_base + ((int)(kseg >> 3) + j) * 16 : zero_off));
+              smem + (kval ? a_base + (sl + (sl >> 2)) * 16 : zero_off));
+        }
       } else if constexpr (kAPieces > 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
+          const int sl = (int)(kseg >> 3) + j;
           const int off = (kval && blk_lane && tok < M)
-                              ? a_base + (((int)(kseg >> 3) + j) * M + tok) * 16
+                              ? a_base + (sl * M + tok + (sl >> 2)) * 16
                               : zero_off;
           a[0][j] = *reinterpret_cast<const u32x4_t*>(smem + off);
         }
@@ -2813,11 +2819,31 @@ int launch_decode_pa(const FwdArgs& p, dim3 grid, int pa, int sets, int lds, hip
     case 1: return launch_decode_inst<FMT, CPW, T, W, 1, 1>(p, grid, lds, stream);
     case 2: return launch_decode_inst<FMT, CPW, T, W, 2, 1>(p, grid, lds, stream);
     case 4: return launch_decode_inst<FMT, CPW, T, W, 4, 1>(p, grid, lds, stream);
+    case 8:
+      if constexpr (FMT != kNF4) return launch_decode_inst<FMT, CPW, T, W, 8, 1>(p, grid, lds, stream);
+      return -1;
     default:
       if constexpr (FMT == kNF4)
         if (sets == 2) return launch_decode_inst<FMT, CPW, T, W, 0, 2>(p, grid, lds, stream);
       return launch_decode_inst<FMT, CPW, T, W, 0, 1>(p, grid, lds, stream);
   }
+}
+
+// LDS staging of a decode launch's activations (eight waves per workgroup):
+// NF4 groups of at most two rows (beside the 64 KiB split table), at most 4
+// pieces of 16 bytes per thread; MXFP4 groups whose padded rows fit two
+// workgroups per CU, at most 8 pieces per thread. Returns the pieces per
+// thread (0: operands load into registers) and the staged bytes.
+template <int FMT>
+int decode_stage(int64_t K, int64_t max_m, int64_t* a_bytes) {
+  constexpr int64_t kThreadsD = 64 * 8;
+  const int64_t pieces = max_m * (K / 8);
+  const int64_t bytes = (pieces + K / 32 + 1) * 16;  // layout of decode_unit
+  const bool stage = FMT == kNF4 ? max_m <= 2 && pieces <= 4 * kThreadsD
+                                 : bytes + 64 <= 80 * 1024 && pieces <= 8 * kThreadsD;
+  *a_bytes = stage ? bytes : 0;
+  if (!stage) return 0;
+  return pieces <= kThreadsD ? 1 : pieces <= 2 * kThreadsD ? 2 : pieces <= 4 * kThreadsD ? 4 : 8;
 }
 
 // Decode launch: one workgroup of eight waves per unit (group, 16 kT rows).
@@ -2833,15 +2859,13 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   if ((int64_t)p.G * n_units > 0x7FFFFFFF || n_units > 0x7FFFFFFF) return -1;
   if (p.G > 65535) return -1;   // grid rows (launch_decode splits larger calls)
   const dim3 grid((unsigned)n_units, (unsigned)p.G, 1);
-  // LDS staging covers at most 4 pieces of 16 bytes per thread
-  const bool stage = p.max_m <= 2 && (int64_t)p.max_m * p.K * 2 <= 4 * 64 * kW * 16;
-  const int64_t a_bytes = stage ? (int64_t)p.max_m * p.K * 2 : 0;
-  const int64_t pieces = (a_bytes + 15) / 16;
-  const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
+  int64_t a_bytes = 0;
+  const int pa = decode_stage<FMT>(p.K, p.max_m, &a_bytes);
+  const bool stage = pa > 0;
   const int sets = FMT != kNF4 ? 1 : p.max_m > 8 ? 2 : (p.max_m == 1 && pa > 0) ? 0 : 1;
   const int64_t red = (int64_t)kW * kT * (sets > 0 ? sets : 1) * 64 * 16;
   const int64_t table = FMT == kNF4 ? kSplitTabBytes : 0;
-  int64_t lds = table + kDecodeFlagBytes + ((a_bytes + 15) & ~15) + 64;
+  int64_t lds = table + kDecodeFlagBytes + (stage ? a_bytes : 0) + 64;
   if (lds < red) lds = red;
   if (lds > 160 * 1024) return -1;
   if (per_wave <= 1) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, sets, (int)lds, stream);
@@ -2860,7 +2884,8 @@ template <int FMT>
 int decode_cpw(int64_t K, int64_t max_m) {
   constexpr int kW = 8;
   const int64_t per_wave = ((K + 127) / 128 + kW - 1) / kW;
-  const bool stage = max_m <= 2 && max_m * K * 2 <= 4 * 64 * kW * 16;
+  int64_t a_bytes = 0;
+  const bool stage = decode_stage<FMT>(K, max_m, &a_bytes) > 0;
   if (per_wave <= 1) return 1;
   if (FMT == kNF4 || per_wave <= 2) return 2;
   if (per_wave <= 3 || !stage) return 3;
@@ -3024,12 +3049,10 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& f
   if (units <= 0) return 0;
   if (units > 0x7FFFFFFF) return -1;
   const int64_t kmax = gu.K > dn.K ? gu.K : dn.K;
-  const bool stage = gu.max_m <= 2 && (int64_t)gu.max_m * kmax * 2 <= 4 * 64 * kW * 16;
-  const int64_t a_bytes = stage ? (int64_t)gu.max_m * kmax * 2 : 0;
-  const int64_t pieces = (a_bytes + 15) / 16;
-  const int pa = !stage ? 0 : pieces <= 512 ? 1 : pieces <= 1024 ? 2 : 4;
+  int64_t a_bytes = 0;
+  const int pa = decode_stage<kNF4>(kmax, gu.max_m, &a_bytes);
   const int sets = gu.max_m > 8 ? 2 : (gu.max_m == 1 && pa > 0) ? 0 : 1;
-  int64_t lds = kSplitTabBytes + kDecodeFlagBytes + ((a_bytes + 15) & ~15) + 64;
+  int64_t lds = kSplitTabBytes + kDecodeFlagBytes + a_bytes + 64;
   const int64_t red = (int64_t)kW * 2 * (sets > 0 ? sets : 1) * 64 * 16;
   if (lds < red) lds = red;
   if (lds > kFfnMaxDynLds) return -1;

@@ -217,6 +217,29 @@ typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4_t;
 __device__ __forceinline__ u32x4_t lds_read16(unsigned addr) {
   return *(lds_u32x4_t*)(size_t)addr;
 }
+// The three bf16 parts of the four bytes of w (lane column lane_off): each
+// part lands straight in its MFMA operand register.
+__device__ __forceinline__ void split_lookup(unsigned w, unsigned lane_off, u32x4_t& hi,
+                                             u32x4_t& mid, u32x4_t& lo) {
+#if GNF4_SPLIT_B32
+  typedef __attribute__((address_space(3))) volatile const uint32_t lds_u32v_t;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const unsigned addr = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0000u | ((4u + b) << 8));
+    hi[b] = *(lds_u32v_t*)(size_t)addr;
+    mid[b] = *(lds_u32v_t*)(size_t)(addr + 4);
+    lo[b] = *(lds_u32v_t*)(size_t)(addr + 8);
+  }
+#else
+  u32x4_t d[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    d[b] = lds_read16(__builtin_amdgcn_perm(w, lane_off, 0x0C0C0000u | ((4u + b) << 8)));
+  hi = u32x4_t{d[0][0], d[1][0], d[2][0], d[3][0]};
+  mid = u32x4_t{d[0][1], d[1][1], d[2][1], d[3][1]};
+  lo = u32x4_t{d[0][2], d[1][2], d[2][2], d[3][2]};
+#endif
+}
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((address_space(3))) const f32x2_t lds_f32x2_t;
 __device__ __forceinline__ f32x2_t lds_read8f(unsigned addr) {
@@ -658,16 +681,8 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
           for (int s = 0; s < kSets; ++s) c[s][0] = c[s][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            u32x4_t d[4];
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-              const unsigned addr =
-                  __builtin_amdgcn_perm(wb[i][t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8));
-              d[b] = lds_read16(addr);
-            }
-            const u32x4_t hi = {d[0][0], d[1][0], d[2][0], d[3][0]};
-            const u32x4_t mid = {d[0][1], d[1][1], d[2][1], d[3][1]};
-            const u32x4_t lo = {d[0][2], d[1][2], d[2][2], d[3][2]};
+            u32x4_t hi, mid, lo;
+            split_lookup(wb[i][t][j], lane_off, hi, mid, lo);
 #pragma unroll
             for (int s = 0; s < kSets; ++s) {
               c[s][j & 1] = mfma(a[s][j], hi, c[s][j & 1]);
@@ -985,14 +1000,8 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
         for (int s = 0; s < kSets; ++s) cs[s][0] = cs[s][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          u32x4_t d[4];
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            d[b] = lds_read16(
-                __builtin_amdgcn_perm(w[t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
-          const u32x4_t hi = {d[0][0], d[1][0], d[2][0], d[3][0]};
-          const u32x4_t mid = {d[0][1], d[1][1], d[2][1], d[3][1]};
-          const u32x4_t lo = {d[0][2], d[1][2], d[2][2], d[3][2]};
+          u32x4_t hi, mid, lo;
+          split_lookup(w[t][j], lane_off, hi, mid, lo);
 #pragma unroll
           for (int s = 0; s < kSets; ++s) {
             cs[s][j & 1] = mfma(a[s][j], hi, cs[s][j & 1]);

@@ -42,10 +42,12 @@ from nf4_grouped import (BLOCKSIZE, DECODE_MAX_ROWS, _aligned_rows, _bf16_activa
 # Auto path choice: the fused launch saves the silu launch and a kernel
 # boundary, and pays a device-scope hand-off per unit (h stores must complete
 # before the flags go out, and down units hold their slot while they wait).
-# Measured on MI355X at Qwen3-30B-A3B shapes (per layer, HIP graph): batch 1
-# 14.4 us fused vs 16.5 us three-launch, batch 4 37.4 vs 39.0, batch 8 63.0
-# vs 60.7 -- the fused launch wins up to about 4000 workgroup units.
-FUSED_MAX_UNITS = 4096
+# Measured on MI355X at Qwen3-30B-A3B shapes (per layer, HIP graph, 112
+# units per group): batch 1 (896 units) 13.7 us fused vs 15.3 us three-launch,
+# batch 2 23.1 vs 22.8, batch 4 48.5 vs 35.3 -- once the batched decode
+# kernels stream well, down units spinning in their slots cost more than the
+# saved launch. The fused launch wins up to about 1000 workgroup units.
+FUSED_MAX_UNITS = 1024
 
 
 def _fused_units(G: int, H: int, n_dn: int) -> int:

@@ -217,20 +217,12 @@ typedef __attribute__((address_space(3))) const u32x4_t lds_u32x4_t;
 __device__ __forceinline__ u32x4_t lds_read16(unsigned addr) {
   return *(lds_u32x4_t*)(size_t)addr;
 }
-// The three bf16 parts of the four bytes of w (lane column lane_off): each
-// part lands straight in its MFMA operand register.
+// The three bf16 parts of the four bytes of w (lane column lane_off), as the
+// hi, mid and lo MFMA operands. One 16-byte read per byte: three separate
+// 4-byte reads per byte into the operand registers measured 1.85x slower
+// (three times the LDS instructions, four lanes per bank).
 __device__ __forceinline__ void split_lookup(unsigned w, unsigned lane_off, u32x4_t& hi,
                                              u32x4_t& mid, u32x4_t& lo) {
-#if GNF4_SPLIT_B32
-  typedef __attribute__((address_space(3))) volatile const uint32_t lds_u32v_t;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const unsigned addr = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0000u | ((4u + b) << 8));
-    hi[b] = *(lds_u32v_t*)(size_t)addr;
-    mid[b] = *(lds_u32v_t*)(size_t)(addr + 4);
-    lo[b] = *(lds_u32v_t*)(size_t)(addr + 8);
-  }
-#else
   u32x4_t d[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b)
@@ -238,7 +230,6 @@ __device__ __forceinline__ void split_lookup(unsigned w, unsigned lane_off, u32x
   hi = u32x4_t{d[0][0], d[1][0], d[2][0], d[3][0]};
   mid = u32x4_t{d[0][1], d[1][1], d[2][1], d[3][1]};
   lo = u32x4_t{d[0][2], d[1][2], d[2][2], d[3][2]};
-#endif
 }
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((address_space(3))) const f32x2_t lds_f32x2_t;

@@ -497,8 +497,10 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   const int a_base = (FMT == kNF4 ? kSplitTabBytes : 0) + kDecodeFlagBytes;
   // staged piece (k / 8, row m) at ((k / 8) M + m + k / 32) x 16 bytes: the
   // extra 16 bytes per 32 elements put the four quarters of a wave's operand
-  // reads on different banks
-  const int zero_off = a_base + (M * kslices + (kslices >> 2) + 1) * 16;
+  // reads on different banks. One row: the row widened to fp32 once here
+  // (32 bytes per piece, at (2 (k / 8) + k / 32) x 16), so the FMAs take
+  // their operands straight from LDS.
+  const int zero_off = a_base + ((kOneRow ? 2 : M) * kslices + (kslices >> 2) + 1) * 16;
 
   // ---- activation staging loads (first in the queue: they are waited on first)
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
@@ -613,7 +615,16 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
         const int pc = (int)threadIdx.x + i * kThreadsD;
         if (wave * 64 + i * kThreadsD < pieces && pc < pieces) {
           const int m = pc / kslices, sl = pc - m * kslices;
-          *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m + (sl >> 2)) * 16) = av[i];
+          if constexpr (kOneRow) {
+            const u32x4_t v = av[i];
+            char* dst = smem + a_base + (2 * sl + (sl >> 2)) * 16;
+            *reinterpret_cast<u32x4_t*>(dst) =
+                u32x4_t{v[0] << 16, v[0] & 0xFFFF0000u, v[1] << 16, v[1] & 0xFFFF0000u};
+            *reinterpret_cast<u32x4_t*>(dst + 16) =
+                u32x4_t{v[2] << 16, v[2] & 0xFFFF0000u, v[3] << 16, v[3] & 0xFFFF0000u};
+          } else {
+            *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m + (sl >> 2)) * 16) = av[i];
+          }
         }
       }
       __syncthreads();
@@ -623,13 +634,15 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
       const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
       const bool kval = kseg < (unsigned)K32;
       u32x4_t a[kSetsA][4];
+      f32x4_t af[kOneRow ? 4 : 1][2];   // one row: fp32 activations
       if constexpr (kOneRow) {
         // every lane: the group's one row over its 32 elements
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int sl = (int)(kseg >> 3) + j;
-          a[0][j] = *reinterpret_cast<const u32x4_t*>(
-              smem + (kval ? a_base + (sl + (sl >> 2)) * 16 : zero_off));
+          const int off = kval ? a_base + (2 * sl + (sl >> 2)) * 16 : zero_off;
+          af[j][0] = *reinterpret_cast<const f32x4_t*>(smem + off);
+          af[j][1] = *reinterpret_cast<const f32x4_t*>(smem + off + 16);
         }
       } else if constexpr (kAPieces > 0) {
 #pragma unroll
@@ -651,17 +664,23 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
         if constexpr (kOneRow) {
           // fp32 codebook pairs times fp32 activations, four chains
           float d[4] = {0.f, 0.f, 0.f, 0.f};
+          // all 16 lookups in flight before the first FMA
+          f32x2_t w[16];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              w[4 * j + b] = lds_read8f(
+                  __builtin_amdgcn_perm(wb[i][t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-              const unsigned addr =
-                  __builtin_amdgcn_perm(wb[i][t][j], lane_off, 0x0C0C0000u | ((4u + b) << 8));
-              const f32x2_t w = lds_read8f(addr);
-              const unsigned x = a[0][j][b];
-              d[2 * (b & 1)] = __builtin_fmaf(w[0], __uint_as_float(x << 16), d[2 * (b & 1)]);
+              const f32x4_t& x = af[j][b >> 1];
+              d[2 * (b & 1)] = __builtin_fmaf(w[4 * j + b][0], x[2 * (b & 1)], d[2 * (b & 1)]);
               d[2 * (b & 1) + 1] =
-                  __builtin_fmaf(w[1], __uint_as_float(x & 0xFFFF0000u), d[2 * (b & 1) + 1]);
+                  __builtin_fmaf(w[4 * j + b][1], x[2 * (b & 1) + 1], d[2 * (b & 1) + 1]);
             }
           acc[t][0][0] = __builtin_fmaf((d[0] + d[1]) + (d[2] + d[3]),
                                         __uint_as_float(sb[i][t]), acc[t][0][0]);
@@ -2838,7 +2857,8 @@ template <int FMT>
 int decode_stage(int64_t K, int64_t max_m, int64_t* a_bytes) {
   constexpr int64_t kThreadsD = 64 * 8;
   const int64_t pieces = max_m * (K / 8);
-  const int64_t bytes = (pieces + K / 32 + 1) * 16;  // layout of decode_unit
+  // layout of decode_unit (one NF4 row: widened to fp32, 32 bytes a piece)
+  const int64_t bytes = ((FMT == kNF4 && max_m == 1 ? 2 : 1) * pieces + K / 32 + 1) * 16;
   const bool stage = FMT == kNF4 ? max_m <= 2 && pieces <= 4 * kThreadsD
                                  : bytes + 64 <= 80 * 1024 && pieces <= 8 * kThreadsD;
   *a_bytes = stage ? bytes : 0;
@@ -2870,6 +2890,8 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   if (lds > 160 * 1024) return -1;
   if (per_wave <= 1) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, sets, (int)lds, stream);
   if constexpr (FMT == kNF4) {
+    // two row sets: one chunk per wave and round (two spill 128 VGPRs)
+    if (sets == 2) return launch_decode_pa<FMT, 1, kT>(p, grid, pa, sets, (int)lds, stream);
     return launch_decode_pa<FMT, 2, kT>(p, grid, pa, sets, (int)lds, stream);
   } else {
     if (per_wave <= 2) return launch_decode_pa<FMT, 2, kT>(p, grid, pa, 1, (int)lds, stream);
@@ -2887,7 +2909,8 @@ int decode_cpw(int64_t K, int64_t max_m) {
   int64_t a_bytes = 0;
   const bool stage = decode_stage<FMT>(K, max_m, &a_bytes) > 0;
   if (per_wave <= 1) return 1;
-  if (FMT == kNF4 || per_wave <= 2) return 2;
+  if (FMT == kNF4) return max_m > 8 ? 1 : 2;   // as launch_decode_t
+  if (per_wave <= 2) return 2;
   if (per_wave <= 3 || !stage) return 3;
   return 4;
 }
@@ -3056,8 +3079,9 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& f
   const int64_t red = (int64_t)kW * 2 * (sets > 0 ? sets : 1) * 64 * 16;
   if (lds < red) lds = red;
   if (lds > kFfnMaxDynLds) return -1;
-  const bool two1 = ((gu.K + 127) / 128 + kW - 1) / kW > 1;
-  const bool two2 = ((dn.K + 127) / 128 + kW - 1) / kW > 1;
+  // chunks per wave as the plain decode launches take them (same bits)
+  const bool two1 = sets != 2 && ((gu.K + 127) / 128 + kW - 1) / kW > 1;
+  const bool two2 = sets != 2 && ((dn.K + 127) / 128 + kW - 1) / kW > 1;
   const uint32_t n = (uint32_t)units;
   if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
   if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);

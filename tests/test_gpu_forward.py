@@ -445,9 +445,12 @@ def test_decode_more_than_65535_one_row_groups(fmt):
                                      ("mxfp4", 640, 1440)])
 def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
     """A group's decoded rows are the same bits in a launch of many units as
-    in a launch of that group alone, and the whole meets the contract.
-    Covers ragged groups, empty groups, a K tail (2880 = 22.5 chunks) and N
-    past a 128-row boundary."""
+    in a launch of that group with only the batch's largest group beside it,
+    and the whole meets the contract. The largest group fixes the launch's
+    class (NF4: one row, up to 8 rows, 9..16 rows: the arithmetic and the
+    chunks per wave differ between classes); within a class no group's bits
+    depend on the others. Covers ragged groups, empty groups, a K tail
+    (2880 = 22.5 chunks) and N past a 128-row boundary."""
     E = 24
     W, S = _stack(fmt, E, N, K, seed=31)
     g = torch.Generator().manual_seed(32)
@@ -455,18 +458,19 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
     sizes = torch.randint(0, 17, (G,), generator=g).tolist()
     sizes[3] = 0
     sizes[5] = 16
+    sizes[7] = 1
     ids = torch.randint(0, E, (G,), generator=g).tolist()
     a = rand_acts(sum(sizes), K, seed=33)
     op = _ops()[fmt]
     out = op(a, W, S, sizes, ids)
-    row = 0
-    for gi in (0, 1, 5, G - 1):
+    r5 = sum(sizes[:5])
+    for gi in (0, 1, 7, G - 1):
         r0 = sum(sizes[:gi])
         m = sizes[gi]
         if m == 0:
             continue
-        alone = op(a[r0:r0 + m], W, S, [m], [ids[gi]])
-        assert torch.equal(out[r0:r0 + m], alone), f"group {gi} differs"
+        pair = op(torch.cat([a[r0:r0 + m], a[r5:r5 + 16]]), W, S, [m, 16], [ids[gi], ids[5]])
+        assert torch.equal(out[r0:r0 + m], pair[:m]), f"group {gi} differs"
     sel = list(range(0, sum(sizes), 7))
     contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel),
                    [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])

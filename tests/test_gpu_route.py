@@ -134,9 +134,12 @@ def _qwen_stack(seed):
     return gu_p, gu_a, dn_p, dn_a
 
 
-def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused):
+def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused, class_rows=None):
     """The reference's MoE block arithmetic with host routing: stable sort by
-    expert, the grouped FFN op on the sorted rows, weighted sum over slots."""
+    expert, the grouped FFN op on the sorted rows, weighted sum over slots.
+    ``class_rows``: run the grouped op in the launch class of that largest
+    group (one extra group of that many zero rows, whose outputs are
+    dropped), as the device-routed path does with its bound min(T, 16)."""
     import nf4_ffn
     T, k = ids.shape
     flat = ids.reshape(-1).cpu()
@@ -145,7 +148,11 @@ def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused):
     eids = torch.nonzero(counts).flatten().tolist()
     sizes = counts[counts > 0].tolist()
     a = x[(order // k).cuda()]
-    y = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, eids, fused=fused)
+    n = a.shape[0]
+    if class_rows is not None and class_rows > max(sizes):
+        a = torch.cat([a, torch.zeros(class_rows, a.shape[1], dtype=a.dtype, device=a.device)])
+        sizes, eids = sizes + [class_rows], eids + [eids[0]]
+    y = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, eids, fused=fused)[:n]
     pos = torch.empty_like(order)
     pos[order] = torch.arange(order.numel())
     pos = pos.cuda().view(T, k)
@@ -163,7 +170,9 @@ def test_moe_ffn_equals_the_host_routed_composition(T):
     logits = torch.randn(T, QWEN["E"], device="cuda")
     ids, w = r.route_topk(logits, QWEN["k"], 0, True)
     out = r.moe_ffn(x, ids, w, gu_p, gu_a, dn_p, dn_a)
-    want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None)
+    # the device path launches in the class of its bound min(T, 16) rows
+    want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None,
+                        class_rows=min(T, 16) if T <= 16 else None)
     assert torch.equal(_bits(out), _bits(want))
     if T <= 16:   # the three-launch decode form over the device tables agrees too
         out3 = r.moe_ffn(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=False)
@@ -231,7 +240,8 @@ def test_moe_layer_from_logits_equals_the_host_routed_composition(T):
     out, ids, w = r.moe_layer(x, logits, QWEN["k"], gu_p, gu_a, dn_p, dn_a, mode=0, norm=True)
     ids2, w2 = r.route_topk(logits, QWEN["k"], 0, True)
     assert torch.equal(ids, ids2) and torch.equal(_bits(w), _bits(w2))
-    want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None)
+    want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None,
+                        class_rows=min(T, 16) if T <= 16 else None)
     assert torch.equal(_bits(out), _bits(want))
 
 

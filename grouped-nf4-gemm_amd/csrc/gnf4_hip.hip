@@ -1100,6 +1100,197 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
   __builtin_amdgcn_s_waitcnt(0);
 }
 
+// A workgroup barrier for LDS only: waits for this wave's LDS operations
+// (lgkmcnt 0), not for its global loads in flight -- __syncthreads() also
+// fences global memory, which waits for every outstanding load. The empty
+// asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------- unit-streaming decode --
+//
+// k_decode_stream<kCpw, kR>: batched MXFP4 decode (groups of 2..16 rows) as
+// a persistent walk over units. Workgroup (x, g) takes a contiguous range
+// of group g's units (32 weight rows each); its eight waves split each
+// unit's K chunks exactly as k_decode_fwd does (wave w: chunks w kCpw ..
+// w kCpw + kCpw - 1, one round) and the unit's partial tiles are reduced
+// through LDS in wave order, so the outputs are k_decode_fwd's bits. What
+// changes is the memory side:
+//   * the group's activation rows are staged into LDS once per workgroup,
+//     not loaded again by every unit (at 9..16 rows k_decode_fwd loads them
+//     into registers per unit: as many load requests as the weights);
+//   * each wave keeps the weight and scale loads of kR units in flight in a
+//     register ring (one workgroup per CU, two waves per SIMD, 256 VGPRs)
+//     and refills a slot as soon as its unit's MFMAs have consumed it, so
+//     the decode, the reduction and the stores of one unit overlap the
+//     loads of the next ones.
+// (The NF4 split-codebook form of this walk measured slower than
+// k_decode_fwd: with two waves per SIMD its LDS lookups are not hidden.)
+// LDS: [activations, padded as in decode_unit][zero block][partial tiles:
+// 8 waves x 2 tiles x 64 lanes x 16 B].
+template <int kCpw, int kR>
+__global__ void __launch_bounds__(512, 1)
+    k_decode_stream(const FwdArgs p, const int upg, const int per_wg) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int kW = 8, kT = 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nl = lane & 15;
+  const int q = lane >> 4;
+  const int g = (int)blockIdx.y;
+  const int u0 = (int)blockIdx.x * per_wg;
+  const int n_units = (upg - u0 < per_wg ? upg - u0 : per_wg);
+  if (n_units <= 0) return;
+
+  int e32, ro_a, ro_b;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(p.eids + g), "s"(p.row_off + g), "s"(p.row_off + g + 1)
+      : "memory");
+  const int64_t e = e32;
+  const int r0 = ro_a;
+  const int M = ro_b - ro_a;
+  if (M <= 0) return;
+  const int K32 = (int)p.K;
+  const int kslices = K32 >> 3;
+  const int pieces = M * kslices;
+  const int zero_off = (pieces + (kslices >> 2) + 1) * 16;
+  const int red_off = zero_off + 64;
+  const int c0 = wave * kCpw;
+
+  // ---- the first eight activation pieces per thread go out before the
+  // ring's loads (the staging then waits for them alone)
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
+  u32x4_t av[8];
+  auto stage_load = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int pc = base + j * 512 + (int)threadIdx.x;
+      const int m = pc / kslices, sl = pc - m * kslices;
+      av[j] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+    }
+  };
+  auto stage_store = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int pc = base + j * 512 + (int)threadIdx.x;
+      if (pc < pieces) {
+        const int m = pc / kslices, sl = pc - m * kslices;
+        *reinterpret_cast<u32x4_t*>(smem + (sl * M + m + (sl >> 2)) * 16) = av[j];
+      }
+    }
+  };
+  stage_load(0);
+
+  // ---- the ring's first kR units
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(static_cast<const uint8_t*>(p.S) + e * p.sse, p.N * p.ssn);
+  u32x4_t wr[kR][kCpw][kT];
+  unsigned sb[kR][kCpw][kT];
+  auto issue = [&](int u, int slot) {
+    // units past the workgroup's range load zeros (offsets past every resource)
+    const bool live = u < n_units;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      const int64_t n = (int64_t)(u0 + u) * (16 * kT) + t * 16 + nl;
+      const bool nok = live && n < p.N;
+      const int b_row = (int)(n * p.sbn), s_row = (int)(n * p.ssn);
+#pragma unroll
+      for (int i = 0; i < kCpw; ++i) {
+        const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+        const bool kval = nok && kseg < (unsigned)K32;
+        wr[slot][i][t] = buf_load16(rb, oob_unless(kval, b_row + (int)(kseg >> 1)));
+        sb[slot][i][t] = buf_load1(rs, oob_unless(kval, s_row + (int)(kseg >> 5)));
+      }
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < kR; ++r) issue(r, r);
+
+  // ---- activations into LDS, once
+  stage_store(0);
+  for (int base = 8 * 512; base < pieces; base += 8 * 512) {
+    stage_load(base);
+    stage_store(base);
+  }
+  if (threadIdx.x < 4)
+    *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
+  lds_barrier();   // the ring's loads stay in flight
+
+  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem + red_off);   // [wave][t][64]
+  // the A operands of the wave's chunks: the same for every unit (token nl)
+  auto a_operand = [&](int i, int j) {
+    const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+    const int sl = (int)(kseg >> 3) + j;
+    const int off = (kseg < (unsigned)K32 && nl < M) ? (sl * M + nl + (sl >> 2)) * 16 : zero_off;
+    return *reinterpret_cast<const u32x4_t*>(smem + off);
+  };
+
+  for (int ub = 0; ub < n_units; ub += kR) {
+#pragma unroll
+    for (int slot = 0; slot < kR; ++slot) {
+      const int u = ub + slot;
+      if (u >= n_units) break;   // uniform across the workgroup
+      // ---- unit u: this wave's run, from ring slot `slot`, in k_decode_fwd's
+      // order (two accumulators per tile, alternate k-slices)
+      f32x4_t acc[kT][2];
+#pragma unroll
+      for (int t = 0; t < kT; ++t) acc[t][0] = acc[t][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kCpw; ++i) {
+        u32x4_t a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = a_operand(i, j);
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          const float sc = e8m0_to_f32(sb[slot][i][t]);
+          u32x4_t b[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) b[j] = mx_dword_to_bf16(wr[slot][i][t][j], sc);
+          acc[t][0] = mfma(a[0], b[0], acc[t][0]);
+          acc[t][1] = mfma(a[1], b[1], acc[t][1]);
+          acc[t][0] = mfma(a[2], b[2], acc[t][0]);
+          acc[t][1] = mfma(a[3], b[3], acc[t][1]);
+        }
+      }
+      // the slot's registers are consumed: refill them with unit u + kR (the
+      // loads write the same registers, so no copy waits for them)
+      issue(u + kR, slot);
+      // ---- the unit's tiles over the waves, in wave order
+      lds_barrier();   // the previous unit's partials have been read
+#pragma unroll
+      for (int t = 0; t < kT; ++t) s_red[(wave * kT + t) * 64 + lane] = acc[t][0] + acc[t][1];
+      lds_barrier();
+      if (wave < kT) {
+        const int t = wave;
+        const f32x4_t* r = s_red + t * 64 + lane;
+        f32x4_t v = r[0];
+#pragma unroll
+        for (int w2 = 1; w2 < kW; ++w2) v = v + r[w2 * kT * 64];
+        const int64_t n = (int64_t)(u0 + u) * (16 * kT) + t * 16 + nl;
+        if (n < p.N) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * q + i;
+            if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+          }
+        }
+      }
+    }
+  }
+  // the ring's last refills (past the range: zero-size offsets) are in flight
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 // ------------------------------------------------------------ fused FFN --
 //
 // gate_up -> silu(gate) * up -> down for groups of at most 16 rows, in one
@@ -2979,6 +3170,52 @@ int launch_rows(const FwdArgs& p, hipStream_t stream) {
   }
 }
 
+template <int CPW, int R>
+int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds,
+                       hipStream_t stream) {
+  static int configured_dev = -1;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -2;
+  if (configured_dev != dev) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode_stream<CPW, R>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+      return -2;
+    configured_dev = dev;
+  }
+  hipLaunchKernelGGL((k_decode_stream<CPW, R>), grid, dim3(512), lds, stream, p, upg, per_wg);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+// Unit-streaming decode (k_decode_stream) for batched MXFP4 launches whose
+// k_decode_fwd form runs three chunks per wave in one round (so the bits
+// agree; GPT-OSS: K = 2880). Each group gets about 256 / G workgroups (one
+// per CU), each a contiguous range of units. Taken when every workgroup
+// walks at least 12 units: measured on MI355X at GPT-OSS-20B shapes, the
+// walk wins from batch 8 (gate_up +3 %) to batch 64 (gate_up 88.1 -> 70.2
+// us, down 48.1 -> 41.2 us) and loses on short walks (batch 4 down -17 %).
+// Returns 1 when the launch is not for it.
+template <int FMT>
+int launch_stream(const FwdArgs& p, hipStream_t stream) {
+  if constexpr (FMT != kMX) {
+    return 1;
+  } else {
+    if (p.max_m < 2 || p.max_m > 16 || p.row_off == nullptr || p.G <= 0 || p.G > 65535) return 1;
+    const int64_t nchunks = (p.K + 127) / 128;
+    if (decode_cpw<FMT>(p.K, p.max_m) != 3 || nchunks > 8 * 3) return 1;
+    const int64_t kslices = p.K / 8;
+    const int64_t lds = ((int64_t)p.max_m * kslices + kslices / 4 + 1) * 16 + 64 + 8 * 2 * 64 * 16;
+    if (lds > 160 * 1024) return 1;
+    const int64_t upg = (p.N + 31) / 32;
+    int64_t wpg = 256 / p.G;
+    if (wpg < 1) wpg = 1;
+    const int64_t per_wg = (upg + wpg - 1) / wpg;
+    if (per_wg < 12) return 1;
+    wpg = (upg + per_wg - 1) / per_wg;
+    const dim3 grid((unsigned)wpg, (unsigned)p.G, 1);
+    return launch_stream_inst<3, 3>(p, grid, (int)upg, (int)per_wg, (int)lds, stream);
+  }
+}
+
 // Unit height: 32 rows, or 16 for single-row MXFP4 groups (more workgroups
 // for a stream that needs little decode work per byte).
 // Groups go to the grid's rows, at most 65535 per launch: larger calls run as
@@ -2987,6 +3224,10 @@ template <int FMT>
 int launch_decode(const FwdArgs& p, hipStream_t stream) {
   {
     const int rc = launch_rows<FMT>(p, stream);
+    if (rc <= 0) return rc;
+  }
+  {
+    const int rc = launch_stream<FMT>(p, stream);
     if (rc <= 0) return rc;
   }
   for (int g0 = 0; g0 < p.G; g0 += 65535) {

@@ -476,6 +476,43 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
                    [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
 
 
+@pytest.mark.parametrize("fmt,N,K,rows", [("nf4", 1536, 2048, 8), ("nf4", 640, 1024, 5),
+                                          ("mxfp4", 5760, 2880, 16), ("mxfp4", 2880, 2880, 9),
+                                          ("mxfp4", 1560, 2880, 3)])
+def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows):
+    """Batched MXFP4 launches at K = 2880 (60 groups of 1..16 rows) run the
+    unit-streaming kernel; a launch of one group runs the per-unit kernel.
+    Both must give the same bits for every group (same chunk split per wave,
+    same reduction order), with ragged groups, an empty group, a partial
+    last unit (N = 1560) and a K tail (22.5 chunks). The NF4 cases check
+    the same invariance for the per-unit kernel alone."""
+    E = 40
+    W, S = _stack(fmt, E, N, K, seed=41)
+    g = torch.Generator().manual_seed(42)
+    G = 60
+    sizes = torch.randint(1, rows + 1, (G,), generator=g).tolist()
+    sizes[2] = 0
+    sizes[4] = rows
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    a = rand_acts(sum(sizes), K, seed=43)
+    op = _ops()[fmt]
+    out = op(a, W, S, sizes, ids)
+    for gi in (0, 1, 4, 17, G - 1):
+        r0, m = sum(sizes[:gi]), sizes[gi]
+        if m == 0:
+            continue
+        # one group alone (NF4: beside a group of the batch's largest size,
+        # which keeps the launch class; two groups still take the per-unit
+        # kernel at these shapes)
+        pad = rows if fmt == "nf4" and m < rows else 0
+        aa = torch.cat([a[r0:r0 + m], a[:pad]]) if pad else a[r0:r0 + m]
+        alone = op(aa, W, S, [m] + ([pad] if pad else []), [ids[gi]] + ([ids[gi]] if pad else []))
+        assert torch.equal(out[r0:r0 + m], alone[:m]), f"group {gi} differs"
+    sel = list(range(0, sum(sizes), 5))
+    contract_check(fmt, out[sel], a[sel], W, S, [1] * len(sel),
+                   [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
+
+
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
 def test_tall_tiles_several_per_workgroup(fmt):
     """More 256-row tiles than the persistent grid has workgroups (64 groups

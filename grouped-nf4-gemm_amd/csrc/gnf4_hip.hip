@@ -1124,7 +1124,7 @@ __device__ __forceinline__ void lds_barrier() {
 //     not loaded again by every unit (at 9..16 rows k_decode_fwd loads them
 //     into registers per unit: as many load requests as the weights);
 //   * each wave keeps the weight and scale loads of kR units in flight in a
-//     register ring (one workgroup per CU, two waves per SIMD, 256 VGPRs)
+//     register ring (one workgroup per CU, two waves per SIMD)
 //     and refills a slot as soon as its unit's MFMAs have consumed it, so
 //     the decode, the reduction and the stores of one unit overlap the
 //     loads of the next ones.
@@ -3191,8 +3191,8 @@ int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds
 // agree; GPT-OSS: K = 2880). Each group gets about 256 / G workgroups (one
 // per CU), each a contiguous range of units. Taken when every workgroup
 // walks at least 12 units: measured on MI355X at GPT-OSS-20B shapes, the
-// walk wins from batch 8 (gate_up +3 %) to batch 64 (gate_up 88.1 -> 70.2
-// us, down 48.1 -> 41.2 us) and loses on short walks (batch 4 down -17 %).
+// walk wins from batch 8 (gate_up +3 %) to batch 64 (gate_up 88.2 -> 69.5
+// us, down 48.2 -> 40.4 us) and loses on short walks (batch 4 down -17 %).
 // Returns 1 when the launch is not for it.
 template <int FMT>
 int launch_stream(const FwdArgs& p, hipStream_t stream) {
@@ -3212,7 +3212,10 @@ int launch_stream(const FwdArgs& p, hipStream_t stream) {
     if (per_wg < 12) return 1;
     wpg = (upg + per_wg - 1) / per_wg;
     const dim3 grid((unsigned)wpg, (unsigned)p.G, 1);
-    return launch_stream_inst<3, 3>(p, grid, (int)upg, (int)per_wg, (int)lds, stream);
+    // a ring of two units per wave: measured against three, four and five
+    // (deeper rings run 1-5 % slower), and against two workgroups per CU
+    // where the staged rows allow it (no faster)
+    return launch_stream_inst<3, 2>(p, grid, (int)upg, (int)per_wg, (int)lds, stream);
   }
 }
 

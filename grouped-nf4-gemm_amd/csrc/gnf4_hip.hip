@@ -1128,8 +1128,9 @@ __device__ __forceinline__ void lds_barrier() {
 //     and refills a slot as soon as its unit's MFMAs have consumed it, so
 //     the decode, the reduction and the stores of one unit overlap the
 //     loads of the next ones.
-// (The NF4 split-codebook form of this walk measured slower than
-// k_decode_fwd: with two waves per SIMD its LDS lookups are not hidden.)
+// (An NF4 split-codebook form of this walk, one or two teams of eight
+// waves, measured 3-8 % slower than k_decode_fwd at Qwen3 batch 8..16: its
+// per-byte LDS lookups need the per-unit kernel's four waves per SIMD.)
 // LDS: [activations, padded as in decode_unit][zero block][partial tiles:
 // 8 waves x 2 tiles x 64 lanes x 16 B].
 template <int kCpw, int kR>

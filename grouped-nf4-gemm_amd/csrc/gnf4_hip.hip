@@ -220,7 +220,8 @@ __device__ __forceinline__ u32x4_t lds_read16(unsigned addr) {
 // The three bf16 parts of the four bytes of w (lane column lane_off), as the
 // hi, mid and lo MFMA operands. One 16-byte read per byte: three separate
 // 4-byte reads per byte into the operand registers measured 1.85x slower
-// (three times the LDS instructions, four lanes per bank).
+// (three times the LDS instructions, four lanes per bank), 12-byte reads
+// 2-10 % slower.
 __device__ __forceinline__ void split_lookup(unsigned w, unsigned lane_off, u32x4_t& hi,
                                              u32x4_t& mid, u32x4_t& lo) {
   u32x4_t d[4];
@@ -1289,6 +1290,178 @@ __global__ void __launch_bounds__(512, 1)
     }
   }
   // the ring's last refills (past the range: zero-size offsets) are in flight
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// k_decode_stream_nf4<kR, kT>: the unit walk for NF4 groups of 2..8 rows
+// (split codebook, one row set, two chunks per wave: 768 < K <= 2048), units
+// of 16 kT weight rows. Two teams of eight waves per workgroup (four waves
+// per SIMD, as k_decode_fwd runs), team t on units t, t + 2, ... of the
+// range. The split table is built and the group's activation rows are
+// staged into LDS once per workgroup, where k_decode_fwd builds the table
+// and loads the activations (into registers) once per unit; each slice's
+// lookups and MFMAs run one at a time (sched_barrier) to stay within 128
+// VGPRs. Same chunk split per wave and reduction order as k_decode_fwd: the
+// same bits. The split decode keeps the LDS busy (16 bytes read per weight
+// byte), so deeper load rings do not pay here: measured on MI355X (Qwen3
+// gate_up), one unit in flight per team, 16-row units: batch 8 33.1 -> 31.8
+// us, batch 16 50.1 -> 47.5..48.7 us; rings of two or three units and
+// 32-row units ran slower.
+template <int kR, int kT>
+__global__ void __launch_bounds__(1024, 1)
+    k_decode_stream_nf4(const FwdArgs p, const int upg, const int per_wg) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int kW = 8, kCpw = 2, kTeams = 2, kThreads = 1024;
+  const int lut = nf4_lut_lane();
+  __builtin_amdgcn_sched_barrier(0);
+  const int lane = threadIdx.x & 63;
+  const int wave = (threadIdx.x >> 6) & (kW - 1);
+  const int team = (int)threadIdx.x >> 9;
+  const int nl = lane & 15;
+  const int q = lane >> 4;
+  const int g = (int)blockIdx.y;
+  const int u0 = (int)blockIdx.x * per_wg;
+  const int n_units = (upg - u0 < per_wg ? upg - u0 : per_wg);
+  if (n_units <= 0) return;
+  int e32, ro_a, ro_b;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(p.eids + g), "s"(p.row_off + g), "s"(p.row_off + g + 1)
+      : "memory");
+  const int64_t e = e32;
+  const int r0 = ro_a;
+  const int M = ro_b - ro_a;
+  if (M <= 0) return;
+  const int K32 = (int)p.K;
+  const int kslices = K32 >> 3;
+  const int pieces = M * kslices;
+  const int a_base = kSplitTabBytes;
+  const int zero_off = a_base + (pieces + (kslices >> 2) + 1) * 16;
+  const int red_off = zero_off + 64 + team * (kW * kT * 64 * 16);
+  const int c0 = wave * kCpw;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.a + (int64_t)r0 * p.lda, (int64_t)M * p.lda * 2);
+  u32x4_t av[4];
+  auto stage_load = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pc = base + j * kThreads + (int)threadIdx.x;
+      const int m = pc / kslices, sl = pc - m * kslices;
+      av[j] = buf_load16(ra, oob_unless(pc < pieces, (int)((int64_t)m * p.lda * 2) + sl * 16));
+    }
+  };
+  auto stage_store = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pc = base + j * kThreads + (int)threadIdx.x;
+      if (pc < pieces) {
+        const int m = pc / kslices, sl = pc - m * kslices;
+        *reinterpret_cast<u32x4_t*>(smem + a_base + (sl * M + m + (sl >> 2)) * 16) = av[j];
+      }
+    }
+  };
+  stage_load(0);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.B + e * p.sbe, p.N * p.sbn);
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(static_cast<const char*>(p.S) + e * p.sse * 4, p.N * p.ssn * 4);
+  u32x4_t wr[kR][kCpw][kT];
+  u32x4_t sq[kR][kT];
+  auto issue = [&](int j, int slot) {
+    const int ul = j * kTeams + team;
+    const bool live = ul < n_units;
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      const int64_t n = (int64_t)(u0 + ul) * (16 * kT) + t * 16 + nl;
+      const bool nok = live && n < p.N;
+      const int b_row = (int)(n * p.sbn), s_row = (int)(n * p.ssn * 4);
+#pragma unroll
+      for (int i = 0; i < kCpw; ++i) {
+        const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+        wr[slot][i][t] =
+            buf_load16(rb, oob_unless(nok && kseg < (unsigned)K32, b_row + (int)(kseg >> 1)));
+      }
+      sq[slot][t] = buf_load16(rs, oob_unless(nok && (unsigned)(c0 * 128) < (unsigned)K32,
+                                              s_row + c0 * 8));
+    }
+  };
+#pragma unroll
+  for (int r = 0; r < kR; ++r) issue(r, r);
+  stage_store(0);
+  for (int base = 4 * kThreads; base < pieces; base += 4 * kThreads) {
+    stage_load(base);
+    stage_store(base);
+  }
+  if (threadIdx.x < 4)
+    *reinterpret_cast<u32x4_t*>(smem + zero_off + threadIdx.x * 16) = u32x4_t{0u, 0u, 0u, 0u};
+  if (threadIdx.x < 512) init_split_table(smem, lut);
+  lds_barrier();
+
+  const bool blk_lane = (nl < 8) == (q < 2);
+  const int tok = nl & 7;
+  const unsigned lane_off = (unsigned)(uintptr_t)smem | (unsigned)(lane & (kSplitCols - 1)) * 16u;
+  f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem + red_off);
+  const int n_steps = (n_units + kTeams - 1) / kTeams;
+  for (int jb = 0; jb < n_steps; jb += kR) {
+#pragma unroll
+    for (int slot = 0; slot < kR; ++slot) {
+      const int j = jb + slot;
+      if (j >= n_steps) break;
+      const int ul = j * kTeams + team;
+      f32x4_t acc[kT];
+#pragma unroll
+      for (int t = 0; t < kT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kCpw; ++i) {
+        const unsigned kseg = (unsigned)((c0 + i) * 128 + q * 32);
+        const bool aval = kseg < (unsigned)K32 && blk_lane && tok < M;
+#pragma unroll
+        for (int t = 0; t < kT; ++t) {
+          const int idx = 2 * i + (q >> 1);
+          const u32x4_t v = sq[slot][t];
+          const float am = __uint_as_float(idx == 0 ? v[0] : idx == 1 ? v[1] : idx == 2 ? v[2] : v[3]);
+          f32x4_t c[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int sl = (int)(kseg >> 3) + jj;
+            const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
+                smem + (aval ? a_base + (sl * M + tok + (sl >> 2)) * 16 : zero_off));
+            u32x4_t hi, mid, lo;
+            split_lookup(wr[slot][i][t][jj], lane_off, hi, mid, lo);
+            c[jj & 1] = mfma(a, hi, c[jj & 1]);
+            c[jj & 1] = mfma(a, mid, c[jj & 1]);
+            c[jj & 1] = mfma(a, lo, c[jj & 1]);
+            __builtin_amdgcn_sched_barrier(0);   // one slice's registers at a time
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(c[0][r] + c[1][r], am, acc[t][r]);
+        }
+      }
+      issue(j + kR, slot);
+      lds_barrier();
+#pragma unroll
+      for (int t = 0; t < kT; ++t) s_red[(wave * kT + t) * 64 + lane] = acc[t];
+      lds_barrier();
+      if (wave < kT && ul < n_units) {
+        const int t = wave;
+        const f32x4_t* r = s_red + t * 64 + lane;
+        f32x4_t v = r[0] + r[32];
+#pragma unroll
+        for (int w2 = 1; w2 < kW; ++w2) v = v + (r[w2 * kT * 64] + r[w2 * kT * 64 + 32]);
+        const int64_t n = (int64_t)(u0 + ul) * (16 * kT) + t * 16 + nl;
+        if (q < 2 && n < p.N) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * q + i;
+            if (m < M) p.out[(int64_t)(r0 + m) * p.ldo + n] = f32_to_bf16_bits(v[i]);
+          }
+        }
+      }
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
 }
 
@@ -3187,7 +3360,9 @@ int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-// Unit-streaming decode (k_decode_stream) for batched MXFP4 launches whose
+// Unit walks for batched decode: k_decode_stream_nf4 for NF4 groups of 2..8
+// rows at 1024 < K <= 2048 (each workgroup walking at least 4 units), and
+// k_decode_stream for batched MXFP4 launches whose
 // k_decode_fwd form runs three chunks per wave in one round (so the bits
 // agree; GPT-OSS: K = 2880). Each group gets about 256 / G workgroups (one
 // per CU), each a contiguous range of units. Taken when every workgroup
@@ -3198,7 +3373,33 @@ int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds
 template <int FMT>
 int launch_stream(const FwdArgs& p, hipStream_t stream) {
   if constexpr (FMT != kMX) {
-    return 1;
+    // NF4: k_decode_stream_nf4, 16-row units, one unit in flight per team
+    if (p.max_m < 2 || p.max_m > 8 || p.row_off == nullptr || p.G <= 0 || p.G > 65535) return 1;
+    const int64_t nchunks = (p.K + 127) / 128;
+    if (decode_cpw<FMT>(p.K, p.max_m) != 2 || nchunks > 16) return 1;   // 1024 < K <= 2048
+    const int64_t kslices = p.K / 8;
+    const int64_t lds = kSplitTabBytes + ((int64_t)p.max_m * kslices + kslices / 4 + 1) * 16 +
+                        64 + 2 * 8 * 64 * 16;
+    if (lds > 160 * 1024) return 1;
+    const int64_t upg = (p.N + 15) / 16;
+    int64_t wpg = 256 / p.G;
+    if (wpg < 1) wpg = 1;
+    const int64_t per_wg = (upg + wpg - 1) / wpg;
+    if (per_wg < 4) return 1;
+    wpg = (upg + per_wg - 1) / per_wg;
+    const dim3 grid((unsigned)wpg, (unsigned)p.G, 1);
+    static int configured_dev = -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -2;
+    if (configured_dev != dev) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_decode_stream_nf4<1, 1>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+        return -2;
+      configured_dev = dev;
+    }
+    hipLaunchKernelGGL((k_decode_stream_nf4<1, 1>), grid, dim3(1024), (int)lds, stream, p,
+                       (int)upg, (int)per_wg);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
   } else {
     if (p.max_m < 2 || p.max_m > 16 || p.row_off == nullptr || p.G <= 0 || p.G > 65535) return 1;
     const int64_t nchunks = (p.K + 127) / 128;

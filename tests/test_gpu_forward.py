@@ -476,16 +476,18 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
                    [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
 
 
-@pytest.mark.parametrize("fmt,N,K,rows", [("nf4", 1536, 2048, 8), ("nf4", 640, 1024, 5),
+@pytest.mark.parametrize("fmt,N,K,rows", [("nf4", 1536, 2048, 8), ("nf4", 648, 1536, 5),
+                                          ("nf4", 640, 1024, 5),
                                           ("mxfp4", 5760, 2880, 16), ("mxfp4", 2880, 2880, 9),
                                           ("mxfp4", 1560, 2880, 3)])
 def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows):
-    """Batched MXFP4 launches at K = 2880 (60 groups of 1..16 rows) run the
-    unit-streaming kernel; a launch of one group runs the per-unit kernel.
-    Both must give the same bits for every group (same chunk split per wave,
-    same reduction order), with ragged groups, an empty group, a partial
-    last unit (N = 1560) and a K tail (22.5 chunks). The NF4 cases check
-    the same invariance for the per-unit kernel alone."""
+    """Batched launches (60 groups) run the unit walks -- MXFP4 at K = 2880
+    (1..16 rows), NF4 at 1024 < K <= 2048 (2..8 rows); a launch of one or
+    two groups runs the per-unit kernel. Both must give the same bits for
+    every group (same chunk split per wave, same reduction order), with
+    ragged groups, an empty group, a partial last unit (N = 1560, 648) and a
+    K tail (MXFP4 22.5 chunks). K = 1024 (one chunk per wave) stays on the
+    per-unit kernel: the invariance holds there too."""
     E = 40
     W, S = _stack(fmt, E, N, K, seed=41)
     g = torch.Generator().manual_seed(42)

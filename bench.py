@@ -401,6 +401,33 @@ def prefill_tflops(dev, seed=0):
     return res
 
 
+def prefill_uniform_tflops(dev, fmt="nf4", m=256, seed=0):
+    """The metric's prefill cell: every expert with m rows (M = 256 per
+    expert), Qwen3 NF4 (128 experts) or GPT-OSS MXFP4 (32 experts), gate_up
+    and down, timed as graph replays of the op."""
+    import torch
+    cfg = QWEN if fmt == "nf4" else GPTOSS
+    E = cfg["E"]
+    make = make_nf4_layers if fmt == "nf4" else make_mx_layers
+    if fmt == "nf4":
+        from nf4_grouped import gemm_4bit_grouped as op
+    else:
+        from mxfp4_grouped import gemm_mxfp4_grouped as op
+    sizes, ids = [m] * E, list(range(E))
+    T = m * E
+    eids = torch.tensor(ids, dtype=torch.int32, device=dev)
+    res = {"rows_per_expert": m, "experts": E}
+    for name, (N, K), s in (("gate_up", cfg["gu"], seed), ("down", cfg["dn"], seed + 1)):
+        (W, S), = make(E, N, K, 1, dev, s)
+        a = torch.randn(T, K, device=dev).to(torch.bfloat16)
+        ms, eager = _timed(lambda: op(a, W, S, sizes, eids), dev)
+        tf = 2.0 * T * N * K / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "tflops": round(tf, 1),
+                     "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "eager_op_ms": round(eager, 4)}
+        del W, S, a
+    return res
+
+
 def dgrad_tflops(dev, seed=0):
     """Config 5: NF4 dgrad on the Qwen3 down projection, 2048 tokens x top-8."""
     import numpy as np
@@ -529,6 +556,7 @@ def main():
         return
     if args.mma_workload:
         log(f"[bench] prefill {json.dumps(prefill_tflops(dev))}")
+        log(f"[bench] prefill m256 {json.dumps(prefill_uniform_tflops(dev, 'nf4'))}")
         log(f"[bench] dgrad {json.dumps(dgrad_tflops(dev))}")
         return
     log(f"[bench] building Qwen3-30B-A3B NF4 decode model: {args.layers} layers, batch {args.batch}")
@@ -577,6 +605,8 @@ def main():
         del mx
         torch.cuda.empty_cache()
         extra["qwen3_nf4_prefill_zipf"] = prefill_tflops(dev)
+        extra["qwen3_nf4_prefill_m256"] = prefill_uniform_tflops(dev, "nf4")
+        extra["gptoss_mxfp4_prefill_m256"] = prefill_uniform_tflops(dev, "mxfp4")
         extra["qwen3_nf4_dgrad_down"] = dgrad_tflops(dev)
         log(f"[bench] extra: {json.dumps(extra)}")
 

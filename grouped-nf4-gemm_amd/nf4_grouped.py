@@ -163,38 +163,53 @@ class _PinnedIndexArena:
 
 
 class _PinnedRing:
-    """Outside capture: a small ring of pinned staging buffers, each guarded
-    by an event, so an index upload is an asynchronous copy that never stalls
-    the host on the GPU (the reference's pageable copy synchronises)."""
+    """Outside capture: a pinned staging ring per (device, stream), so an
+    index upload is an asynchronous copy that never stalls the host on the
+    GPU (the reference's pageable copy synchronises). The ring is cut into
+    PARTS parts; an event is recorded on the stream when the ring leaves a
+    part, and the host waits for that event before it writes into the part
+    again (long done in practice). Values go in through a numpy view of the
+    pinned memory (no temporary tensor)."""
 
-    SLOTS = 8
+    INTS = 1 << 16
+    PARTS = 8
 
     def __init__(self):
-        self.slots = [None] * self.SLOTS
-        self.events = [None] * self.SLOTS
-        self.i = 0
+        self.host = torch.empty(self.INTS, dtype=torch.int32, pin_memory=True)
+        self.np = self.host.numpy()
+        self.events = [None] * self.PARTS
+        self.part = 0     # the part being filled
+        self.off = 0      # next free int in it
         self.lock = threading.Lock()
 
-    def stage(self, flat: list, dev):
+    def stage(self, flat, dev, stream):
+        n = len(flat)
+        size = self.INTS // self.PARTS
         with self.lock:
-            i = self.i
-            self.i = (i + 1) % self.SLOTS
-            ev = self.events[i]
-            if ev is not None:
-                ev.synchronize()              # the copy that last used this slot
-            buf = self.slots[i]
-            n = len(flat)
-            if buf is None or buf.numel() < n:
-                buf = torch.empty(max(n, 4096), dtype=torch.int32, pin_memory=True)
-                self.slots[i] = buf
-            host = buf[:n]
-            host.copy_(torch.from_numpy(flat) if isinstance(flat, np.ndarray)
-                       else torch.tensor(flat, dtype=torch.int32))
-            out = host.to(dev, non_blocking=True)
-            if ev is None:
+            if n > size:
+                # larger than a part (not on any launch path's shapes): a
+                # pinned buffer of its own, kept until its copy has run
+                host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+                host.numpy()[:] = flat
+                out = host.to(dev, non_blocking=True)
                 ev = torch.cuda.Event()
-                self.events[i] = ev
-            ev.record(torch.cuda.current_stream(dev))
+                ev.record(stream)
+                ev.synchronize()
+                return out
+            if self.off + n > size:
+                ev = self.events[self.part]
+                if ev is None:
+                    ev = self.events[self.part] = torch.cuda.Event()
+                ev.record(stream)                      # after this part's copies
+                self.part = (self.part + 1) % self.PARTS
+                self.off = 0
+                nxt = self.events[self.part]
+                if nxt is not None:
+                    nxt.synchronize()                  # its last round's copies ran
+            base = self.part * size + self.off
+            self.np[base:base + n] = flat
+            out = self.host[base:base + n].to(dev, non_blocking=True)
+            self.off += n
             return out
 
 
@@ -209,11 +224,12 @@ def _arena(device) -> _PinnedIndexArena:
     return _ARENAS[key]
 
 
-def _ring(device) -> _PinnedRing:
-    key = str(device)
-    if key not in _RINGS:
-        _RINGS[key] = _PinnedRing()
-    return _RINGS[key]
+def _ring(device, stream) -> _PinnedRing:
+    key = (str(device), stream.cuda_stream)
+    ring = _RINGS.get(key)
+    if ring is None:
+        ring = _RINGS[key] = _PinnedRing()
+    return ring
 
 
 def to_device_i32(seqs, device):
@@ -244,7 +260,8 @@ def to_device_i32(seqs, device):
                        else torch.tensor(flat, dtype=torch.int32))
             packed = host.to(dev, non_blocking=True)
         else:
-            packed = _ring(dev).stage(flat, dev)
+            stream = torch.cuda.current_stream(dev)
+            packed = _ring(dev, stream).stage(flat, dev, stream)
     out, off = [], 0
     for n in lens:
         out.append(packed[off:off + n])

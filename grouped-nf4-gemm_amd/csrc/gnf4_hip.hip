@@ -2635,15 +2635,27 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
       uniform_ptr(out + (int64_t)t.row0 * p.ldo), 0, uniform((int)((int64_t)t.rows * p.ldo * 2)),
       0x00020000);
   const int ldo2 = (int)(p.ldo * 2);
+  // whole 8-column chunks store 16 bytes; the chunk that straddles the
+  // output width (width % 8 == 4) stores its first 8 bytes only, so no
+  // store reaches past a row's last column
   const int chunk = lane & 31;
   const int col = t.n0 + chunk * 8;
-  const int coff = col < Nout ? col * 2 + h * ldo2 : kOOB;
+  const int coff16 = col + 8 <= Nout ? col * 2 + h * ldo2 : kOOB;
+  const int coff8 = col < Nout && col + 8 > Nout ? col * 2 + h * ldo2 : kOOB;
+  const bool straddle = Nout % 8 != 0;
   // wave w stores rows 2 (4 j + w) + lane / 32, j = 0 .. 4 kM - 1
 #pragma unroll
   for (int j = 0; j < kM * 4; ++j) {
     const int row = (j * 4 + wave) * 2 + h;
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + row * 512 + ((chunk ^ (row & 31)) << 4));
-    __builtin_amdgcn_raw_buffer_store_b128(v, ro, coff, uniform((j * 4 + wave) * 2 * ldo2), 0);
+    const int so = uniform((j * 4 + wave) * 2 * ldo2);
+    __builtin_amdgcn_raw_buffer_store_b128(v, ro, coff16, so, 0);
+    if (straddle) {
+      u32x2_t v2;
+      v2.x = v[0];
+      v2.y = v[1];
+      __builtin_amdgcn_raw_buffer_store_b64(v2, ro, coff8, so, 0);
+    }
   }
 }
 

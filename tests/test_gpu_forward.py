@@ -406,11 +406,12 @@ def test_tall_tiles_give_the_bits_of_128_row_tiles(fmt, sizes):
 
 
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
-@pytest.mark.parametrize("N,K", [(320, 704), (2880, 2880), (96, 64)])
+@pytest.mark.parametrize("N,K", [(320, 704), (2880, 2880), (96, 64), (260, 256), (1540, 384)])
 def test_tall_tiles_ragged_weight_rows_and_step_counts(fmt, N, K):
     """The four-wave tall-tile kernel with weight rows that do not fill its
     256-row tile (N % 256 != 0), step counts that are not multiples of the
-    three-slot load rings (K / 64 = 11, 45, 1) and every row-subtile class
+    three-slot load rings (K / 64 = 11, 45, 1), output widths that end
+    inside an 8-column store chunk (N % 8 == 4) and every row-subtile class
     (<= 64, <= 128, > 128 rows): bitwise equal to 128-row tiles."""
     sizes = [300, 40, 0, 100, 256, 129]
     W, S = _stack(fmt, 6, N, K, seed=71)

@@ -143,24 +143,6 @@ __device__ __forceinline__ u32x4_t nf4_dword_to_bf16_at(const char* lds0, unsign
   return r;
 }
 
-// 32 NF4 elements (16 packed bytes) -> 4 MFMA operands. All 16 table reads
-// are issued before any is used, so one LDS round trip covers the chunk.
-__device__ __forceinline__ void nf4_16bytes_to_bf16(const float2* tab, u32x4_t w, unsigned lane_off,
-                                                    float s, u32x4_t (&out)[4]) {
-  float2 p[16];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const unsigned addr = __builtin_amdgcn_perm(w[j], lane_off, 0x0C0C0000u | ((4u + i) << 8));
-      p[4 * j + i] = *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(tab) + addr);
-    }
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[j][i] = bf16x2_bits(p[4 * j + i].x * s, p[4 * j + i].y * s);
-}
-
 // ---- exact three-part NF4 codebook (decode kernels) ----
 //
 // Every fp32 codebook value v splits exactly into three bf16 values,
@@ -318,10 +300,6 @@ constexpr int kScopeDevice = 16;
 template <int kAux>
 __device__ __forceinline__ u32x4_t buf_load16_aux(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAux));
-}
-
-__device__ __forceinline__ unsigned buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
 __device__ __forceinline__ unsigned buf_load1(__amdgpu_buffer_rsrc_t r, int off) {
@@ -1781,10 +1759,6 @@ template <int n>
 __device__ __forceinline__ void wait_vm_lgkm0() {
   static_assert(n >= 0 && n < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
-}
-
-__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

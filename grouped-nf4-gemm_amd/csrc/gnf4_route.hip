@@ -43,11 +43,6 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float((uint32_t)b << 16);
 }
 
-// (value, index) order of the selection: larger value first, then lower index.
-__device__ __forceinline__ bool beats(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
-}
-
 // Wave-wide reductions on the DPP network: xor-1 and xor-2 quad
 // permutes, the half-row and row mirrors, then row broadcasts 15 and 31
 // carry each row's result into the next rows; lane 63 ends with the whole

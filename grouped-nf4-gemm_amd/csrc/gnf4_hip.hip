@@ -3379,6 +3379,16 @@ int launch_stream(const FwdArgs& p, hipStream_t stream) {
     const int64_t per_wg = (upg + wpg - 1) / wpg;
     if (per_wg < 4) return 1;
     wpg = (upg + per_wg - 1) / per_wg;
+    // Whole workgroups per group leave CUs idle for some group counts
+    // (G = 86 on 256 CUs: 2 per group, 172 busy). The walk's time follows
+    // its longest range (per_wg units), the per-unit kernel's the total
+    // (it spreads every unit over every CU); measured at Qwen3 gate_up
+    // shapes (G = 60..120, 1..4 rows): walk ~ 0.96 us x per_wg + 10.7 us,
+    // per-unit ~ 5.4 ns x units + 7.9 us, so the walk runs where
+    // units >= CUs x (0.7 per_wg + 2).
+    const int cus = device_cus();
+    if (cus <= 0) return -2;
+    if (upg * p.G * 10 < (int64_t)cus * (7 * per_wg + 20)) return 1;
     const dim3 grid((unsigned)wpg, (unsigned)p.G, 1);
     static int configured_dev = -1;
     int dev = 0;

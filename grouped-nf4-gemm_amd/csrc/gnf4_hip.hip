@@ -3771,6 +3771,13 @@ int gnf4_hip_abi_version(void) { return GNF4_HIP_ABI_VERSION; }
 
 int gnf4_hip_device_cus(void) { return device_cus(); }
 
+int gnf4_hip_copy_to_device(void* dst, const void* src, int64_t bytes, void* stream) {
+  if (bytes < 0 || (bytes > 0 && (!dst || !src))) return -1;
+  if (bytes == 0) return 0;
+  return hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice,
+                        static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -2;
+}
+
 int gnf4_hip_activations_to_bf16(const void* src, int src_dtype, int64_t rows, int64_t cols,
                                  int64_t ld_src, void* dst, int64_t ld_dst, void* stream) {
   if (src_dtype != GNF4_DTYPE_F16 && src_dtype != GNF4_DTYPE_F32) return -1;

@@ -30,6 +30,7 @@ tiles tied with it).
 """
 from __future__ import annotations
 
+import contextlib
 import os
 
 import numpy as np
@@ -213,8 +214,96 @@ class _PinnedRing:
             return out
 
 
+class _TableRing:
+    """Outside capture, the launch paths' group tables (expert ids, row
+    offsets, tile table) per (device, stream): a pinned host ring and a
+    device ring of the same size. A call writes its ints into the host ring
+    through a numpy view, one stream-ordered copy moves them into the device
+    ring, and the kernel reads them there; no tensor is made per call. Both
+    rings are cut into PARTS parts; an event recorded on the stream when the
+    ring leaves a part guards both sides of that part (its copies, and every
+    kernel enqueued before the event, have run when it completes), and the
+    host waits for it before writing into the part again (long done in
+    practice)."""
+
+    INTS = 1 << 16
+    PARTS = 8
+
+    def __init__(self, dev):
+        self.host = torch.empty(self.INTS, dtype=torch.int32, pin_memory=True)
+        self.np = self.host.numpy()
+        self.dev = torch.empty(self.INTS, dtype=torch.int32, device=dev)
+        self.host_ptr = self.host.data_ptr()
+        self.dev_ptr = self.dev.data_ptr()
+        self.events = [None] * self.PARTS
+        self.part = 0
+        self.off = 0
+        self.lock = threading.Lock()
+
+    def stage(self, tables, stream):
+        """Device pointers of `tables` (int sequences / int32 numpy arrays),
+        in order (0 for an empty one); None when they do not fit a part."""
+        lens = [len(t) for t in tables]
+        n = sum(lens)
+        size = self.INTS // self.PARTS
+        if n > size:
+            return None
+        with self.lock:
+            if self.off + n > size:
+                ev = self.events[self.part]
+                if ev is None:
+                    ev = self.events[self.part] = torch.cuda.Event()
+                ev.record(stream)
+                self.part = (self.part + 1) % self.PARTS
+                self.off = 0
+                nxt = self.events[self.part]
+                if nxt is not None:
+                    nxt.synchronize()
+            base = self.part * size + self.off
+            ptrs, b = [], base
+            for t, ln in zip(tables, lens):
+                if ln:
+                    self.np[b:b + ln] = t.numpy() if torch.is_tensor(t) else t
+                ptrs.append(self.dev_ptr + 4 * b if ln else 0)
+                b += ln
+            _hiplib.check(_hiplib.load().gnf4_hip_copy_to_device(
+                self.dev_ptr + 4 * base, self.host_ptr + 4 * base, 4 * n, stream.cuda_stream),
+                "group-table upload")
+            self.off += n
+            return ptrs
+
+
 _ARENAS: dict = {}
 _RINGS: dict = {}
+_TABLE_RINGS: dict = {}
+
+
+def _table_ring(dev, stream) -> _TableRing:
+    key = (str(dev), stream.cuda_stream)
+    ring = _TABLE_RINGS.get(key)
+    if ring is None:
+        ring = _TABLE_RINGS[key] = _TableRing(dev)
+    return ring
+
+
+def _upload_tables(tables, dev, stream):
+    """Device pointers of one launch's int32 tables, and what must stay
+    alive until the launch is enqueued: the table ring outside capture,
+    ``to_device_i32``'s capture-safe path inside one (or for tables too
+    large for a ring part)."""
+    if not _PinnedIndexArena._capturing():
+        ptrs = _table_ring(dev, stream).stage(tables, stream)
+        if ptrs is not None:
+            return ptrs, None
+    views = to_device_i32(tables, dev)
+    return [v.data_ptr() if v.numel() else 0 for v in views], views
+
+
+def _device_ctx(dev):
+    """``torch.cuda.device(dev)``, or nothing when dev is already current."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def _arena(device) -> _PinnedIndexArena:
@@ -627,39 +716,36 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
     host_eids = [] if eids_dev is not None else expert_ids
+    stream = torch.cuda.current_stream(dev)
     if max_m <= DECODE_MAX_ROWS and block_m is None:
         if min(sizes_i) == 1 and max_m == 1:
             # one row per group: group g is row g, no offset table to upload
-            (e_h,) = to_device_i32((host_eids,), dev)
+            (e_p,), keep = _upload_tables((host_eids,), dev, stream)
             r_ptr = None
-            keep = (e_h,)
         else:
             row_off = [0]
             for m in sizes_i:
                 row_off.append(row_off[-1] + m)
-            e_h, r_h = to_device_i32((host_eids, row_off), dev)
-            r_ptr = r_h.data_ptr()
-            keep = (e_h, r_h)
-        eids = eids_dev if eids_dev is not None else e_h
+            (e_p, r_ptr), keep = _upload_tables((host_eids, row_off), dev, stream)
+        e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
         # decode path: block_m carries the largest group size
-        args = (eids.data_ptr(), r_ptr, G, None, None, None, 0, max_m)
+        args = (e_ptr, r_ptr, G, None, None, None, 0, max_m)
     else:
         bm = _fwd_block_m(max_m, N, K, block_m)
         t0, tr, tg = _tiles_np(sizes_i, bm)
         if bm == 256:
             t0, tr, tg = _xcd_balanced(t0, tr, tg)
-        e_h, t0_d, tr_d, tg_d = to_device_i32((_np_ids(host_eids), t0, tr, tg), dev)
-        eids = eids_dev if eids_dev is not None else e_h
-        args = (eids.data_ptr(), None, G, t0_d.data_ptr(), tr_d.data_ptr(),
-                tg_d.data_ptr(), len(t0), bm)
-        keep = (e_h, t0_d, tr_d, tg_d, eids)
-    with torch.cuda.device(dev):
+        (e_p, t0_p, tr_p, tg_p), keep = _upload_tables((_np_ids(host_eids), t0, tr, tg), dev,
+                                                       stream)
+        e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
+        args = (e_ptr, None, G, t0_p, tr_p, tg_p, len(t0), bm)
+    with _device_ctx(dev):
         rc = lib.gnf4_hip_grouped_fwd(
             fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
             W.data_ptr(), W.stride(0), W.stride(1),
             S.data_ptr(), S.stride(0), S.stride(1),
-            *args, N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
-    del keep  # index tensors stay alive until the launch is enqueued
+            *args, N, K, out.data_ptr(), out.stride(0), stream.cuda_stream)
+    del keep, eids_dev  # index tensors stay alive until the launch is enqueued
     _hiplib.check(rc, op)
     return out
 
@@ -697,15 +783,17 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     eids_dev = _eids_device(expert_ids, dev)
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
-    e_h, t0_d, tr_d, tg_d = to_device_i32((_np_ids([] if eids_dev is not None else expert_ids),
-                                           t0, tr, tg), dev)
-    eids = eids_dev if eids_dev is not None else e_h
-    with torch.cuda.device(dev):
+    stream = torch.cuda.current_stream(dev)
+    (e_p, t0_p, tr_p, tg_p), keep = _upload_tables(
+        (_np_ids([] if eids_dev is not None else expert_ids), t0, tr, tg), dev, stream)
+    e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
+    with _device_ctx(dev):
         rc = lib.gnf4_hip_grouped_dgrad(
             fmt, g.data_ptr(), _hiplib.DTYPE_BF16, g.stride(0),
             W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
-            eids.data_ptr(), t0_d.data_ptr(), tr_d.data_ptr(), tg_d.data_ptr(), len(t0), bm,
-            N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+            e_ptr, t0_p, tr_p, tg_p, len(t0), bm,
+            N, K, out.data_ptr(), out.stride(0), stream.cuda_stream)
+    del keep, eids_dev
     _hiplib.check(rc, op)
     return out
 

@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 5
+#define GNF4_HIP_ABI_VERSION 6
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -63,6 +63,15 @@ int gnf4_hip_abi_version(void);
 /* Compute units of the current device (0 on error). Replaces the reference's
  * torch-side SM query `_sm_count` (kernel/nf4_grouped.py:581-591). */
 int gnf4_hip_device_cus(void);
+
+/* Stream-ordered copy of `bytes` bytes of pinned host memory to device memory
+ * (hipMemcpyAsync on `stream`): the upload of one call's group tables (expert
+ * ids, row offsets, tile table) into a device staging ring, without a torch
+ * tensor per call. The reference uploads the same tables with a torch copy
+ * (to_device_i32, kernel/nf4_grouped.py:229-331). The host bytes must stay
+ * unchanged until the copy has run. 0 on success, -1 on bad arguments, -2 on
+ * a runtime error. */
+int gnf4_hip_copy_to_device(void *dst, const void *src, int64_t bytes, void *stream);
 
 /* Round fp16 (src_dtype GNF4_DTYPE_F16) or fp32 (GNF4_DTYPE_F32) activations
  * [rows, ld_src] to bf16 [rows, ld_dst], nearest-even (NaN -> 0x7FC0), so a

@@ -534,3 +534,27 @@ def test_tall_tiles_several_per_workgroup(fmt):
     short = op(a, W, S, sizes, ids, block_m=128)
     assert torch.equal(tall, short)
     contract_check(fmt, tall, a, W, S, sizes, ids)
+
+
+def test_group_table_ring_wraps_without_reuse_races():
+    """Eager calls upload their group tables through a pinned ring and a
+    device ring (eight parts, event-guarded). 1200 back-to-back calls
+    alternating two routings wrap the rings more than twice; every output
+    must equal its routing's first result bit for bit, with no host sync
+    between the launches."""
+    from nf4_grouped import gemm_4bit_grouped
+    W, S = _stack("nf4", 32, 256, 512, seed=91)
+    g = torch.Generator().manual_seed(92)
+    routes = []
+    for _ in range(2):
+        sizes = torch.randint(1, 4, (64,), generator=g).tolist()
+        ids = torch.randint(0, 32, (64,), generator=g).tolist()
+        routes.append((sizes, ids, rand_acts(sum(sizes), 512, seed=93)))
+    refs = [gemm_4bit_grouped(a, W, S, sizes, ids) for sizes, ids, a in routes]
+    outs = []
+    for i in range(1200):
+        sizes, ids, a = routes[i % 2]
+        outs.append(gemm_4bit_grouped(a, W, S, sizes, ids))
+    torch.cuda.synchronize()
+    for i, o in enumerate(outs):
+        assert torch.equal(o, refs[i % 2]), f"call {i} differs"

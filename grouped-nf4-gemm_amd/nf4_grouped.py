@@ -292,6 +292,9 @@ def _upload_tables(tables, dev, stream):
     ``to_device_i32``'s capture-safe path inside one (or for tables too
     large for a ring part)."""
     if not _PinnedIndexArena._capturing():
+        # the capture path's pinned arena must exist before any capture
+        # starts (allocating it inside one would invalidate the capture)
+        _arena(dev)
         ptrs = _table_ring(dev, stream).stage(tables, stream)
         if ptrs is not None:
             return ptrs, None

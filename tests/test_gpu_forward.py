@@ -558,3 +558,39 @@ def test_group_table_ring_wraps_without_reuse_races():
     torch.cuda.synchronize()
     for i, o in enumerate(outs):
         assert torch.equal(o, refs[i % 2]), f"call {i} differs"
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+def test_op_captures_after_one_eager_call(fmt):
+    """An eager call (tables through the staging rings) followed by a graph
+    capture of the same op (tables through the capture-safe pinned arena,
+    which the eager call must have created): the capture succeeds and its
+    replays give the eager bits, for the decode and the tiled paths."""
+    import nf4_grouped
+    op = _ops()[fmt]
+    W, S = _stack(fmt, 8, 256, 512, seed=95)
+    # as in a fresh process: no arena yet (earlier tests' arenas are set
+    # aside, not freed, and restored afterwards)
+    saved = dict(nf4_grouped._ARENAS)
+    nf4_grouped._ARENAS.clear()
+    graphs = []
+    try:
+        for sizes, ids in (([2, 1, 3], [1, 5, 7]), ([40, 300, 7], [2, 4, 6])):
+            a = rand_acts(sum(sizes), 512, seed=96)
+            eager = op(a, W, S, sizes, ids)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = op(a, W, S, sizes, ids)
+            graphs.append(graph)
+            for _ in range(3):
+                graph.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager)
+    finally:
+        torch.cuda.synchronize()
+        fresh = dict(nf4_grouped._ARENAS)
+        del graphs
+        nf4_grouped._ARENAS.clear()
+        nf4_grouped._ARENAS.update(saved)
+        del fresh

@@ -37,7 +37,7 @@ import _hiplib
 import nf4_grouped
 from nf4_grouped import (BLOCKSIZE, DECODE_MAX_ROWS, _aligned_rows, _bf16_activations,
                          _check_host_ids, _eids_device, _require_gpu, _scales_view,
-                         _stream_ptr, to_device_i32)
+                         _stream_ptr)
 
 # Auto path choice: the fused launch saves the silu launch and a kernel
 # boundary, and pays a device-scope hand-off per unit (h stores must complete
@@ -209,18 +209,19 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     for m in sizes_i:
         row_off.append(row_off[-1] + m)
     host_eids = [] if eids_dev is not None else expert_ids
-    e_h, r_h = to_device_i32((host_eids, row_off), dev)
-    eids = eids_dev if eids_dev is not None else e_h
-    out = _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, r_h, G, max_m)
-    del e_h, r_h   # the index tensors stay alive until the launch is enqueued
+    (e_p, r_p), keep = nf4_grouped._upload_tables((host_eids, row_off), dev,
+                                                  torch.cuda.current_stream(dev))
+    eids = eids_dev.data_ptr() if eids_dev is not None else e_p
+    out = _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, r_p, G, max_m)
+    del keep, eids_dev   # the index tensors stay alive until the launch is enqueued
     return out
 
 
 def _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, row_off, G: int,
                   max_m: int, h=None, out=None, op="gemm_nf4_ffn_grouped"):
     """The fused kernel over device group tables (``eids [G]`` and
-    ``row_off [G + 1]`` int32; ``max_m`` an upper bound of the largest group,
-    <= 16). ``a`` bf16 [T, K]."""
+    ``row_off [G + 1]`` int32, as tensors or device addresses; ``max_m`` an
+    upper bound of the largest group, <= 16). ``a`` bf16 [T, K]."""
     T, K = a.shape
     H, n_dn = gu_packed.shape[1] // 2, dn_packed.shape[1]
     dev = a.device
@@ -236,7 +237,9 @@ def _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, row_off, 
             a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
             Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
             Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
-            eids.data_ptr(), row_off.data_ptr(), G, max(max_m, 1), 2 * H, K, n_dn,
+            eids if isinstance(eids, int) else eids.data_ptr(),
+            row_off if isinstance(row_off, int) else row_off.data_ptr(), G, max(max_m, 1),
+            2 * H, K, n_dn,
             h.data_ptr(), h.stride(0), sync.data_ptr(), sync.numel(),
             out.data_ptr(), out.stride(0), _stream_ptr(dev))
     _hiplib.check(rc, op)

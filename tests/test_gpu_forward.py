@@ -517,6 +517,29 @@ def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows, G):
                    [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
 
 
+def test_streamed_mxfp4_scales_off_16_byte_alignment():
+    """The MXFP4 unit walk moves each unit's scale bytes through LDS with
+    16-byte loads when the scale stack is 16-byte aligned, and loads them per
+    lane otherwise. Scales one byte off alignment take the per-lane form:
+    the same bits as the aligned stack, and as the per-unit kernel."""
+    N, K, rows, G, E = 1560, 2880, 3, 60, 40
+    W, S = _stack("mxfp4", E, N, K, seed=51)
+    buf = torch.empty(S.numel() + 1, dtype=torch.uint8, device=S.device)
+    S1 = buf[1:].view(S.shape)
+    S1.copy_(S)
+    assert S1.data_ptr() % 16 != 0
+    g = torch.Generator().manual_seed(52)
+    sizes = torch.randint(1, rows + 1, (G,), generator=g).tolist()
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    a = rand_acts(sum(sizes), K, seed=53)
+    op = _ops()["mxfp4"]
+    out = op(a, W, S, sizes, ids)
+    assert torch.equal(op(a, W, S1, sizes, ids), out)
+    for gi in (0, 7, G - 1):
+        r0, m = sum(sizes[:gi]), sizes[gi]
+        assert torch.equal(out[r0:r0 + m], op(a[r0:r0 + m], W, S1, [m], [ids[gi]])), gi
+
+
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
 def test_tall_tiles_several_per_workgroup(fmt):
     """More 256-row tiles than the persistent grid has workgroups (64 groups

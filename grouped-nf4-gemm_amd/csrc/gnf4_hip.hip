@@ -3410,10 +3410,12 @@ int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds
 // k_decode_stream for batched MXFP4 launches whose
 // k_decode_fwd form runs three chunks per wave in one round (so the bits
 // agree; GPT-OSS: K = 2880). Each group gets about 256 / G workgroups (one
-// per CU), each a contiguous range of units. Taken when every workgroup
-// walks at least 12 units: measured on MI355X at GPT-OSS-20B shapes, the
-// walk wins from batch 8 (gate_up +3 %) to batch 64 (gate_up 88.2 -> 69.5
-// us, down 48.2 -> 40.4 us) and loses on short walks (batch 4 down -17 %).
+// per CU), each a contiguous range of units. MXFP4 takes it when every
+// workgroup walks at least 4 units: measured on MI355X at GPT-OSS-20B
+// shapes against the per-unit kernel, batch 3 / 4 gate_up 24.6 / 30.5 ->
+// 22.9 / 27.5 us, batch 6 / 8 down 22.5 / 25.1 -> 20.7 / 22.8 us, batch 64
+// gate_up 88.2 -> 61.9 us; walks of 2..3 units (batch 2 down) run 2 %
+// slower.
 // Returns 1 when the launch is not for it.
 template <int FMT>
 int launch_stream(const FwdArgs& p, hipStream_t stream) {
@@ -3466,7 +3468,7 @@ int launch_stream(const FwdArgs& p, hipStream_t stream) {
     int64_t wpg = 256 / p.G;
     if (wpg < 1) wpg = 1;
     const int64_t per_wg = (upg + wpg - 1) / wpg;
-    if (per_wg < 12) return 1;
+    if (per_wg < 4) return 1;
     wpg = (upg + per_wg - 1) / per_wg;
     const dim3 grid((unsigned)wpg, (unsigned)p.G, 1);
     // a ring of two units per wave: measured against three, four and five

@@ -481,10 +481,12 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
                                             ("nf4", 1536, 2048, 3, 86), ("nf4", 640, 1024, 5, 60),
                                             ("mxfp4", 5760, 2880, 16, 60),
                                             ("mxfp4", 2880, 2880, 9, 60),
-                                            ("mxfp4", 1560, 2880, 3, 60)])
+                                            ("mxfp4", 1560, 2880, 3, 60),
+                                            ("mxfp4", 1560, 2880, 4, 20)])
 def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows, G):
-    """Batched launches (60 or 86 groups) run the unit walks -- MXFP4 at
-    K = 2880 (1..16 rows), NF4 at 1024 < K <= 2048 (2..8 rows); a launch of
+    """Batched launches (20..86 groups) run the unit walks -- MXFP4 at
+    K = 2880 (1..16 rows; 20 groups: walks of 5 units), NF4 at
+    1024 < K <= 2048 (2..8 rows); a launch of
     one or two groups runs the per-unit kernel. Both must give the same bits
     for every group (NF4: all of them; same chunk split per wave, same
     reduction order), with

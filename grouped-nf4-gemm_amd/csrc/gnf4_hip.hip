@@ -842,7 +842,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
 
 // ------------------------------------------------- row-streaming decode --
 //
-// k_decode_rows<FMT, kW, kT, kSets, kCpw, kR, kP>: decode (every group <= 16
+// k_decode_rows<FMT, kW, kT, kSets, kCpw, kR, kP, kAbsBlock>: decode (every group <= 16
 // rows) for launches with many groups (batched decode). Each wave owns
 // 16 kT weight rows of one group over the whole K, so no partial sums cross
 // waves: the wave streams its rows' 128-element chunks through a register
@@ -864,7 +864,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
 // k_decode_fwd launch takes when the launch needs one round), each run
 // summed in its own chain, the runs added in order. So both kernels -- and
 // the fused FFN, which runs decode_unit -- give identical outputs.
-template <int FMT, int kW, int kT, int kSets, int kCpw, int kR, int kP>
+template <int FMT, int kW, int kT, int kSets, int kCpw, int kR, int kP, bool kAbsBlock>
 __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr bool kSplit = FMT == kNF4;
@@ -929,8 +929,24 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
     s_row[t] = n[t] < p.N ? (int)(n[t] * p.ssn * kScaleBytes) + (FMT == kNF4 ? 0 : q) : kOOB;
   }
   u32x4_t wr[kD][kT];
-  u32x4_t sq[kSplit ? kD / 2 : 1][kT];   // NF4 absmax of chunk pairs
+  u32x4_t sq[kSplit && !kAbsBlock ? kD / 2 : 1][kT];   // NF4 absmax of chunk pairs
   unsigned sb[kSplit ? 1 : kD][kT];      // MXFP4 scale bytes
+  // NF4 with kAbsBlock: the absmax of a tile's 16 rows (16 x K / 64 floats,
+  // contiguous, at most 1 KiB) comes in as one coalesced load, ahead of the
+  // ring, lane L holding floats 4 L .. 4 L + 3; a chunk pair's four floats
+  // of row nl then sit in one lane (the row length is a multiple of 4) and
+  // reach lane (nl, q) through four ds_bpermute. The per-pair loads put 16
+  // rows' lines into each load: as many requests as the weight loads.
+  constexpr bool abs_block = kSplit && kAbsBlock;
+  const int abs_row = (int)p.ssn;   // floats
+  u32x4_t sgl[kT];
+  if constexpr (abs_block) {
+#pragma unroll
+    for (int t = 0; t < kT; ++t) {
+      const int64_t n0 = (int64_t)blockIdx.x * (16 * kW * kT) + (wave * kT + t) * 16;
+      sgl[t] = buf_load16(rs, oob_unless(n0 < p.N, (int)(n0 * abs_row * 4) + lane * 16));
+    }
+  }
   auto issue = [&](int c, int slot) {
     // past the end of K (the second half of a last 64-element chunk, or the
     // ring's refills beyond the last chunk): zeros
@@ -939,7 +955,8 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
     for (int t = 0; t < kT; ++t) {
       wr[slot][t] = buf_load16(rb, oob_unless(ok, b_row[t] + c * 64));
       if constexpr (kSplit) {
-        if ((slot & 1) == 0)
+        if constexpr (!abs_block)
+          if ((slot & 1) == 0)
           sq[slot / 2][t] = buf_load16(rs, oob_unless((unsigned)(c * 128) < (unsigned)K32,
                                                       s_row[t] + c * 8));
       } else {
@@ -1060,7 +1077,17 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
           if constexpr (kSplit) {
             // absmax block 2 c + q / 2: element 2 (c % 2) + q / 2 of the pair's
             // four; a lane past the end of K multiplies zeros by zero
-            if ((slot & 1) == 0) pair_sq[t] = sq[slot / 2][t];
+            if ((slot & 1) == 0) {
+              if constexpr (abs_block) {
+                // floats 4 h .. 4 h + 3 of row nl (h = c / 2): lane (nl ssn + 4 h) / 4
+                const int src = (nl * abs_row + 2 * c) & ~3;   // bytes: lane x 4
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                  pair_sq[t][k] = (unsigned)__builtin_amdgcn_ds_bpermute(src, (int)sgl[t][k]);
+              } else {
+                pair_sq[t] = sq[slot / 2][t];
+              }
+            }
             const u32x4_t v = pair_sq[t];
             const unsigned lo2 = (slot & 1) ? v[2] : v[0], hi2 = (slot & 1) ? v[3] : v[1];
             scl[t] = kval ? __uint_as_float(q >= 2 ? hi2 : lo2) : 0.f;
@@ -3328,20 +3355,20 @@ int decode_cpw(int64_t K, int64_t max_m) {
 // Row-streaming decode (k_decode_rows) for a launch whose k_decode_fwd
 // form needs one round per wave (so the two kernels' bits agree); returns 1
 // when this launch is not for it.
-template <int FMT, int W, int T, int S, int CPW, int R, int P>
+template <int FMT, int W, int T, int S, int CPW, int R, int P, bool AB>
 int launch_rows_inst(const FwdArgs& p, int lds, hipStream_t stream) {
   static int configured_dev = -1;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return -2;
   if (configured_dev != dev) {
     if (hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&k_decode_rows<FMT, W, T, S, CPW, R, P>),
+            reinterpret_cast<const void*>(&k_decode_rows<FMT, W, T, S, CPW, R, P, AB>),
             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
       return -2;
     configured_dev = dev;
   }
   const dim3 grid((unsigned)((p.N + 16 * W * T - 1) / (16 * W * T)), (unsigned)p.G, 1);
-  hipLaunchKernelGGL((k_decode_rows<FMT, W, T, S, CPW, R, P>), grid, dim3(64 * W), lds, stream,
+  hipLaunchKernelGGL((k_decode_rows<FMT, W, T, S, CPW, R, P, AB>), grid, dim3(64 * W), lds, stream,
                      p);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
@@ -3351,7 +3378,12 @@ template <int FMT, int W, int S, int P>
 int launch_rows_cpw(const FwdArgs& p, int cpw, int lds, hipStream_t stream) {
   // (fewer than 8 chunks: k_decode_fwd runs one chunk per wave)
   if (cpw != 1) return 1;
-  return launch_rows_inst<FMT, W, 2, S, 1, 2, P>(p, lds, stream);
+  // absmax as whole 16-row blocks where a block fits one 1 KiB load, its
+  // rows are a multiple of 4 floats and the loads are aligned
+  const bool ab = p.ssn % 4 == 0 && p.ssn <= 16 && p.sse % 4 == 0 &&
+                  reinterpret_cast<uintptr_t>(p.S) % 16 == 0;
+  if (ab) return launch_rows_inst<FMT, W, 2, S, 1, 2, P, true>(p, lds, stream);
+  return launch_rows_inst<FMT, W, 2, S, 1, 2, P, false>(p, lds, stream);
 }
 
 // Taken for NF4 launches of groups of 2..8 rows whose K gives k_decode_fwd's
@@ -3380,12 +3412,13 @@ int launch_rows(const FwdArgs& p, hipStream_t stream) {
   if (pp > 8) return 1;
   const int P = pp <= 2 ? 2 : pp <= 4 ? 4 : 8;
   (void)sets;
-  if (two) return P == 2 ? launch_rows_cpw<FMT, 8, 1, 2>(p, cpw, (int)lds, stream)
-                 : P == 4 ? launch_rows_cpw<FMT, 8, 1, 4>(p, cpw, (int)lds, stream)
-                          : launch_rows_cpw<FMT, 8, 1, 8>(p, cpw, (int)lds, stream);
-  return P == 2 ? launch_rows_cpw<FMT, 16, 1, 2>(p, cpw, (int)lds, stream)
-         : P == 4 ? launch_rows_cpw<FMT, 16, 1, 4>(p, cpw, (int)lds, stream)
-                  : launch_rows_cpw<FMT, 16, 1, 8>(p, cpw, (int)lds, stream);
+  const FwdArgs& q = p;
+  if (two) return P == 2 ? launch_rows_cpw<FMT, 8, 1, 2>(q, cpw, (int)lds, stream)
+                 : P == 4 ? launch_rows_cpw<FMT, 8, 1, 4>(q, cpw, (int)lds, stream)
+                          : launch_rows_cpw<FMT, 8, 1, 8>(q, cpw, (int)lds, stream);
+  return P == 2 ? launch_rows_cpw<FMT, 16, 1, 2>(q, cpw, (int)lds, stream)
+         : P == 4 ? launch_rows_cpw<FMT, 16, 1, 4>(q, cpw, (int)lds, stream)
+                  : launch_rows_cpw<FMT, 16, 1, 8>(q, cpw, (int)lds, stream);
   }
 }
 
@@ -3998,7 +4031,7 @@ int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const
       !aligned16(a))
     return -1;
   if (n_mtiles > 0 && (!t_row0 || !t_rows || !t_group)) return -1;
-  FwdArgs p;
+  FwdArgs p{};
   p.a = static_cast<const uint16_t*>(a);
   p.lda = lda;
   p.B = B;

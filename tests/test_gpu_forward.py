@@ -542,6 +542,29 @@ def test_streamed_mxfp4_scales_off_16_byte_alignment():
         assert torch.equal(out[r0:r0 + m], op(a[r0:r0 + m], W, S1, [m], [ids[gi]])), gi
 
 
+def test_row_stream_nf4_absmax_off_16_byte_alignment():
+    """The NF4 row-streaming decode (K = 768, groups of 2..8 rows) reads a
+    tile's absmax as one coalesced 16-row block when the absmax stack is
+    16-byte aligned, and per chunk pair otherwise: an absmax stack one float
+    off alignment gives the same bits."""
+    N, K, G, E = 2048, 768, 40, 16
+    W, S = _stack("nf4", E, N, K, seed=61)
+    buf = torch.empty(S.numel() + 1, dtype=S.dtype, device=S.device)
+    S1 = buf[1:].view(S.shape)
+    S1.copy_(S)
+    assert S1.data_ptr() % 16 != 0
+    g = torch.Generator().manual_seed(62)
+    sizes = torch.randint(2, 9, (G,), generator=g).tolist()
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    a = rand_acts(sum(sizes), K, seed=63)
+    op = _ops()["nf4"]
+    out = op(a, W, S, sizes, ids)
+    assert torch.equal(op(a, W, S1, sizes, ids), out)
+    sel = list(range(0, sum(sizes), 3))
+    contract_check("nf4", out[sel], a[sel], W, S, [1] * len(sel),
+                   [ids[next(i for i in range(G) if sum(sizes[:i + 1]) > r)] for r in sel])
+
+
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
 def test_tall_tiles_several_per_workgroup(fmt):
     """More 256-row tiles than the persistent grid has workgroups (64 groups

@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -29,6 +29,7 @@ SIGNATURES = {
     "gnf4_hip_abi_version": [],
     "gnf4_hip_device_cus": [],
     "gnf4_hip_copy_to_device": [_P, _P, _I64, _P],
+    "gnf4_hip_host_device_address": [_P, _P],
     "gnf4_hip_activations_to_bf16": [_P, _I, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_ffn_sync_words": [_I, _I64, _I64],

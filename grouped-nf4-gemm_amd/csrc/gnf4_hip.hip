@@ -3875,6 +3875,17 @@ int gnf4_hip_copy_to_device(void* dst, const void* src, int64_t bytes, void* str
                         static_cast<hipStream_t>(stream)) == hipSuccess ? 0 : -2;
 }
 
+int gnf4_hip_host_device_address(const void* host, void** device) {
+  if (!host || !device) return -1;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, const_cast<void*>(host), 0) != hipSuccess || !d) {
+    (void)hipGetLastError();
+    return -2;
+  }
+  *device = d;
+  return 0;
+}
+
 int gnf4_hip_activations_to_bf16(const void* src, int src_dtype, int64_t rows, int64_t cols,
                                  int64_t ld_src, void* dst, int64_t ld_dst, void* stream) {
   if (src_dtype != GNF4_DTYPE_F16 && src_dtype != GNF4_DTYPE_F32) return -1;

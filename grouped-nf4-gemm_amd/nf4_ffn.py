@@ -210,7 +210,7 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
         row_off.append(row_off[-1] + m)
     host_eids = [] if eids_dev is not None else expert_ids
     (e_p, r_p), keep = nf4_grouped._upload_tables((host_eids, row_off), dev,
-                                                  torch.cuda.current_stream(dev))
+                                                  torch.cuda.current_stream(dev), host_ok=True)
     eids = eids_dev.data_ptr() if eids_dev is not None else e_p
     out = _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, r_p, G, max_m)
     del keep, eids_dev   # the index tensors stay alive until the launch is enqueued

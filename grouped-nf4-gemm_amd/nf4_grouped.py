@@ -31,6 +31,7 @@ tiles tied with it).
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import os
 
 import numpy as np
@@ -218,13 +219,15 @@ class _TableRing:
     """Outside capture, the launch paths' group tables (expert ids, row
     offsets, tile table) per (device, stream): a pinned host ring and a
     device ring of the same size. A call writes its ints into the host ring
-    through a numpy view, one stream-ordered copy moves them into the device
-    ring, and the kernel reads them there; no tensor is made per call. Both
-    rings are cut into PARTS parts; an event recorded on the stream when the
-    ring leaves a part guards both sides of that part (its copies, and every
-    kernel enqueued before the event, have run when it completes), and the
-    host waits for it before writing into the part again (long done in
-    practice)."""
+    through a numpy view; no tensor is made per call. Decode launches
+    (``host_ok``: each workgroup reads its group's three words once) read
+    them there, at the ring's device address, with no copy; tile launches,
+    which read their tile table once per tile, get one stream-ordered copy
+    into the device ring. Both rings are cut into PARTS parts; an event
+    recorded on the stream when the ring leaves a part guards both sides of
+    that part (its copies, and every kernel enqueued before the event, have
+    run when it completes), and the host waits for it before writing into
+    the part again (long done in practice)."""
 
     INTS = 1 << 16
     PARTS = 8
@@ -235,14 +238,20 @@ class _TableRing:
         self.dev = torch.empty(self.INTS, dtype=torch.int32, device=dev)
         self.host_ptr = self.host.data_ptr()
         self.dev_ptr = self.dev.data_ptr()
+        addr = ctypes.c_void_p()
+        with _device_ctx(dev):
+            rc = _hiplib.load().gnf4_hip_host_device_address(self.host_ptr, ctypes.byref(addr))
+        # None: the host ring is not mapped for the device (every call copies)
+        self.host_dev_ptr = addr.value if rc == 0 else None
         self.events = [None] * self.PARTS
         self.part = 0
         self.off = 0
         self.lock = threading.Lock()
 
-    def stage(self, tables, stream):
+    def stage(self, tables, stream, host_ok=False):
         """Device pointers of `tables` (int sequences / int32 numpy arrays),
-        in order (0 for an empty one); None when they do not fit a part."""
+        in order (0 for an empty one); None when they do not fit a part.
+        `host_ok`: the pointers may address the pinned host ring."""
         lens = [len(t) for t in tables]
         n = sum(lens)
         size = self.INTS // self.PARTS
@@ -260,15 +269,18 @@ class _TableRing:
                 if nxt is not None:
                     nxt.synchronize()
             base = self.part * size + self.off
+            direct = host_ok and self.host_dev_ptr is not None
+            at = self.host_dev_ptr if direct else self.dev_ptr
             ptrs, b = [], base
             for t, ln in zip(tables, lens):
                 if ln:
                     self.np[b:b + ln] = t.numpy() if torch.is_tensor(t) else t
-                ptrs.append(self.dev_ptr + 4 * b if ln else 0)
+                ptrs.append(at + 4 * b if ln else 0)
                 b += ln
-            _hiplib.check(_hiplib.load().gnf4_hip_copy_to_device(
-                self.dev_ptr + 4 * base, self.host_ptr + 4 * base, 4 * n, stream.cuda_stream),
-                "group-table upload")
+            if not direct:
+                _hiplib.check(_hiplib.load().gnf4_hip_copy_to_device(
+                    self.dev_ptr + 4 * base, self.host_ptr + 4 * base, 4 * n,
+                    stream.cuda_stream), "group-table upload")
             self.off += n
             return ptrs
 
@@ -286,16 +298,17 @@ def _table_ring(dev, stream) -> _TableRing:
     return ring
 
 
-def _upload_tables(tables, dev, stream):
+def _upload_tables(tables, dev, stream, host_ok=False):
     """Device pointers of one launch's int32 tables, and what must stay
-    alive until the launch is enqueued: the table ring outside capture,
-    ``to_device_i32``'s capture-safe path inside one (or for tables too
-    large for a ring part)."""
+    alive until the launch is enqueued: the table ring outside capture
+    (`host_ok`: read from its pinned host side), ``to_device_i32``'s
+    capture-safe path inside one (or for tables too large for a ring
+    part)."""
     if not _PinnedIndexArena._capturing():
         # the capture path's pinned arena must exist before any capture
         # starts (allocating it inside one would invalidate the capture)
         _arena(dev)
-        ptrs = _table_ring(dev, stream).stage(tables, stream)
+        ptrs = _table_ring(dev, stream).stage(tables, stream, host_ok)
         if ptrs is not None:
             return ptrs, None
     views = to_device_i32(tables, dev)
@@ -723,13 +736,14 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
     if max_m <= DECODE_MAX_ROWS and block_m is None:
         if min(sizes_i) == 1 and max_m == 1:
             # one row per group: group g is row g, no offset table to upload
-            (e_p,), keep = _upload_tables((host_eids,), dev, stream)
+            (e_p,), keep = _upload_tables((host_eids,), dev, stream, host_ok=True)
             r_ptr = None
         else:
             row_off = [0]
             for m in sizes_i:
                 row_off.append(row_off[-1] + m)
-            (e_p, r_ptr), keep = _upload_tables((host_eids, row_off), dev, stream)
+            (e_p, r_ptr), keep = _upload_tables((host_eids, row_off), dev, stream,
+                                                host_ok=True)
         e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
         # decode path: block_m carries the largest group size
         args = (e_ptr, r_ptr, G, None, None, None, 0, max_m)

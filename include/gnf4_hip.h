@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 6
+#define GNF4_HIP_ABI_VERSION 7
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -72,6 +72,15 @@ int gnf4_hip_device_cus(void);
  * unchanged until the copy has run. 0 on success, -1 on bad arguments, -2 on
  * a runtime error. */
 int gnf4_hip_copy_to_device(void *dst, const void *src, int64_t bytes, void *stream);
+
+/* The device address of pinned host memory (hipHostGetDevicePointer): decode
+ * launches read their group tables (expert ids, row offsets) straight from a
+ * pinned host ring at this address, with no copy; each workgroup reads its
+ * group's three words once. The reference uploads the same tables with a
+ * torch copy (to_device_i32, kernel/nf4_grouped.py:229-331). 0 on success,
+ * -1 on bad arguments, -2 when the memory is not mapped for the current
+ * device. */
+int gnf4_hip_host_device_address(const void *host, void **device);
 
 /* Round fp16 (src_dtype GNF4_DTYPE_F16) or fp32 (GNF4_DTYPE_F32) activations
  * [rows, ld_src] to bf16 [rows, ld_dst], nearest-even (NaN -> 0x7FC0), so a

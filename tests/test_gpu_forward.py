@@ -585,27 +585,34 @@ def test_tall_tiles_several_per_workgroup(fmt):
 
 
 def test_group_table_ring_wraps_without_reuse_races():
-    """Eager calls upload their group tables through a pinned ring and a
-    device ring (eight parts, event-guarded). 1200 back-to-back calls
-    alternating two routings wrap the rings more than twice; every output
-    must equal its routing's first result bit for bit, with no host sync
+    """Eager calls stage their group tables in a pinned ring (eight parts,
+    event-guarded): decode launches read them there at the ring's device
+    address, tile launches from a device copy. 1200 back-to-back calls
+    cycling two decode routings and one tiled routing wrap the ring more
+    than twice; every output must equal its routing's result computed from
+    device-resident expert ids (no ring) bit for bit, with no host sync
     between the launches."""
+    import nf4_grouped
     from nf4_grouped import gemm_4bit_grouped
     W, S = _stack("nf4", 32, 256, 512, seed=91)
     g = torch.Generator().manual_seed(92)
     routes = []
-    for _ in range(2):
-        sizes = torch.randint(1, 4, (64,), generator=g).tolist()
-        ids = torch.randint(0, 32, (64,), generator=g).tolist()
-        routes.append((sizes, ids, rand_acts(sum(sizes), 512, seed=93)))
-    refs = [gemm_4bit_grouped(a, W, S, sizes, ids) for sizes, ids, a in routes]
+    for lo, hi, G in ((1, 4, 64), (1, 4, 64), (150, 300, 6)):
+        sizes = torch.randint(lo, hi, (G,), generator=g).tolist()
+        ids = torch.randint(0, 32, (G,), generator=g).tolist()
+        routes.append((sizes, ids, rand_acts(sum(sizes), 512, seed=93 + G)))
+    refs = [gemm_4bit_grouped(a, W, S, sizes, torch.tensor(ids, dtype=torch.int32, device="cuda"))
+            for sizes, ids, a in routes]
     outs = []
     for i in range(1200):
-        sizes, ids, a = routes[i % 2]
+        sizes, ids, a = routes[i % 3]
         outs.append(gemm_4bit_grouped(a, W, S, sizes, ids))
     torch.cuda.synchronize()
+    ring = nf4_grouped._table_ring(torch.device("cuda", torch.cuda.current_device()),
+                                   torch.cuda.current_stream())
+    assert ring.host_dev_ptr is not None, "the pinned ring is not mapped for the device"
     for i, o in enumerate(outs):
-        assert torch.equal(o, refs[i % 2]), f"call {i} differs"
+        assert torch.equal(o, refs[i % 3]), f"call {i} differs"
 
 
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])

@@ -3,6 +3,10 @@
  *
  * Plain pointers and sizes only. All pointers are device pointers except
  * `stream`, which is a hipStream_t (pass torch.cuda.current_stream().cuda_stream).
+ * The group tables of a decode-path launch (expert_ids, row_off) may also
+ * be pinned host memory at its device address (gnf4_hip_host_device_address):
+ * each workgroup reads its group's words once. Tile tables should be device
+ * memory: the tiled kernels read them once per tile.
  * Every call is asynchronous and stream-ordered; none allocates or synchronises.
  *
  * Shared conventions (reference docs/KERNEL_CONTRACT.md, kernel/nf4_grouped.py:697-725):

@@ -267,13 +267,13 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     eids[g] = 0;
     row_off[g] = (int32_t)N;
   }
+  __syncthreads();   // every wave's atomicMax on s_max has landed
   if (tid == 0) {
     row_off[slots] = (int32_t)N;
     info[0] = active;
     info[1] = s_max;
     info[2] = s_bad;
   }
-  __syncthreads();
   // (4) stable placement, 64 rows at a time per wave
   for (int c0 = r0; c0 < r1; c0 += 64) {
     const int i = c0 + lane;

@@ -627,8 +627,8 @@ def _check_host_ids(expert_ids, E: int) -> None:
     """Host-side expert ids must index the stack: an out-of-range id would
     make the kernel read outside the weights. Device-resident ids are the
     caller's responsibility (checking them would synchronise)."""
-    ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else list(expert_ids)
-    if ids and (min(int(e) for e in ids) < 0 or max(int(e) for e in ids) >= E):
+    ids = expert_ids.tolist() if torch.is_tensor(expert_ids) else expert_ids
+    if len(ids) and (int(min(ids)) < 0 or int(max(ids)) >= E):
         raise ValueError(f"expert id out of range [0, {E})")
 
 

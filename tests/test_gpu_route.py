@@ -231,6 +231,26 @@ def test_one_launch_prologue_equals_the_separate_kernels(T, E, k, mode, norm):
     assert torch.equal(plan3.order, plan2.order) and torch.equal(_bits(a3), _bits(a))
 
 
+def test_group_info_counts_every_wave_largest_group():
+    """info[1], the largest group, reflects every wave's experts: with 512
+    experts the grouping kernel's experts span eight waves, and the largest
+    group sits on an expert of a late wave (ids >= 64) in every trial (the
+    summary word is written only after all waves' maxima have landed)."""
+    r = _route()
+    g = torch.Generator().manual_seed(5)
+    for trial in range(200):
+        T, k, E = 3, 8, 512
+        ids = torch.randperm(E - 64, generator=g)[:T * k].add(64).view(T, k)
+        big = int(ids[0, 0])
+        ids[1, 0] = big                      # one expert of two rows
+        if trial % 2:
+            ids[2, 0] = big                  # or three
+        plan = r.route_groups(ids.to("cuda", torch.int64), E)
+        want = int(torch.bincount(ids.flatten(), minlength=E).max())
+        got = plan.info.cpu().tolist()
+        assert got[1] == want and got[0] == len(set(ids.flatten().tolist())), (trial, got, want)
+
+
 @pytest.mark.parametrize("T", [1, 8, 24])
 def test_moe_layer_from_logits_equals_the_host_routed_composition(T):
     r = _route()

@@ -1225,8 +1225,8 @@ __global__ void __launch_bounds__(512, 1)
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(static_cast<const uint8_t*>(p.S) + e * p.sse, p.N * p.ssn);
   u32x4_t wr[kR][kCpw][kT];
-  // (bytes: held as 32-bit values the compiler re-masks them at the loop's
-  // back edge, which waits for the newest loads)
+  // (bytes: held as 32-bit values they get re-masked at the loop's back
+  // edge, and the mask waits for the newest loads)
   uint8_t sb[kR][kCpw][kT];
   u32x4_t sg[kR];   // kLdsScales, waves 0..2: 1 KiB each of the unit's scale block
   auto issue = [&](int u, int slot) {

@@ -615,6 +615,33 @@ def test_group_table_ring_wraps_without_reuse_races():
         assert torch.equal(o, refs[i % 3]), f"call {i} differs"
 
 
+def test_group_tables_on_two_streams():
+    """Each stream stages its calls' group tables in its own pinned ring.
+    Decode calls alternating between two side streams (no sync between
+    them, 600 calls of 129 table words each, so both rings wrap) match the
+    device-id results bit for bit."""
+    from nf4_grouped import gemm_4bit_grouped
+    W, S = _stack("nf4", 32, 256, 512, seed=95)
+    g = torch.Generator().manual_seed(96)
+    sizes = torch.randint(1, 4, (64,), generator=g).tolist()
+    ids = [torch.randint(0, 32, (64,), generator=g).tolist() for _ in range(2)]
+    a = rand_acts(sum(sizes), 512, seed=97)
+    refs = [gemm_4bit_grouped(a, W, S, sizes, torch.tensor(i, dtype=torch.int32, device="cuda"))
+            for i in ids]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s_ in streams:
+        s_.wait_stream(torch.cuda.current_stream())
+    outs = [[], []]
+    for i in range(1200):
+        j = i % 2
+        with torch.cuda.stream(streams[j]):
+            outs[j].append(gemm_4bit_grouped(a, W, S, sizes, ids[j]))
+    torch.cuda.synchronize()
+    for j in range(2):
+        for i, o in enumerate(outs[j]):
+            assert torch.equal(o, refs[j]), (j, i)
+
+
 @pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
 def test_op_captures_after_one_eager_call(fmt):
     """An eager call (tables through the staging rings) followed by a graph

@@ -108,6 +108,40 @@ __device__ __forceinline__ void init_pair_table(float2* tab, int lut) {
   for (int j = 0; j < nj; ++j) tab[b * 32 + ((j0 + j + b) & 31)] = e;
 }
 
+// Codebook value c (0..15) from immediate constants (a select chain): no
+// memory load, so a table built from it need not wait for any.
+__device__ __forceinline__ float nf4_code_imm(unsigned c) {
+  float r = -1.0f;
+  r = c == 1 ? -0.6961928009986877f : r;
+  r = c == 2 ? -0.5250730514526367f : r;
+  r = c == 3 ? -0.39491748809814453f : r;
+  r = c == 4 ? -0.28444138169288635f : r;
+  r = c == 5 ? -0.18477343022823334f : r;
+  r = c == 6 ? -0.09105003625154495f : r;
+  r = c == 7 ? 0.0f : r;
+  r = c == 8 ? 0.07958029955625534f : r;
+  r = c == 9 ? 0.16093020141124725f : r;
+  r = c == 10 ? 0.24611230194568634f : r;
+  r = c == 11 ? 0.33791524171829224f : r;
+  r = c == 12 ? 0.44070982933044434f : r;
+  r = c == 13 ? 0.5626170039176941f : r;
+  r = c == 14 ? 0.7229568362236023f : r;
+  r = c == 15 ? 1.0f : r;
+  return r;
+}
+
+// The pair table of init_pair_table (64 KiB at LDS offset 0, 32 lane
+// columns) filled by 512 threads from nf4_code_imm: thread t fills 16
+// columns of byte t % 256.
+__device__ __forceinline__ void init_pair_table_imm(char* smem) {
+  const unsigned b = threadIdx.x & 255;
+  const float2 e = make_float2(nf4_code_imm(b >> 4), nf4_code_imm(b & 15));
+  const int j0 = threadIdx.x < 256 ? 0 : 16;
+  float2* tab = reinterpret_cast<float2*>(smem);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) tab[b * 32 + ((j0 + j + b) & 31)] = e;
+}
+
 __device__ __forceinline__ unsigned bf16x2_bits(float lo, float hi) {
   bf16x2_t r = {(__bf16)lo, (__bf16)hi};  // v_cvt_pk_bf16_f32, RNE
   return __builtin_bit_cast(unsigned, r);
@@ -382,6 +416,47 @@ __device__ __forceinline__ float bf16_round(float f) {
   return __uint_as_float((uint32_t)f32_to_bf16_bits(f) << 16);
 }
 
+// ---- one-row (GEMV) summation order, shared by every kernel that computes
+// an NF4 group of exactly one row (k_gemv_nf4, and decode_unit with row
+// sets 0, which the fused FFN runs), so their outputs are bit-identical.
+// A row of K elements is PR = K / 32 pieces of 32 elements (16 packed bytes).
+//   * piece p: h_p = (d0 + d1) + (d2 + d3), where byte m (0..15) of the
+//     piece adds LUT[hi] * a[2m] to chain 2 (m % 2) and LUT[lo] * a[2m + 1]
+//     to chain 2 (m % 2) + 1 (fp32 FMAs, bytes in order), and x_p = h_p *
+//     absmax[p / 2] (one fp32 multiply);
+//   * slots: LR = 32 lanes for PR <= 32, else 64; slot j sums x_j, x_{j+LR},
+//     x_{j+2LR}, ... in that order (pieces past the row add nothing, a slot
+//     with no piece holds +0);
+//   * the LR slots are added by a fixed tree: pairs (j, j ^ 32) (LR = 64),
+//     then (j, j ^ 16), (j, j ^ 8), (j, j ^ 7) within eight, (j, j ^ 2),
+//     (j, j ^ 1).
+// The tree is what a wave's cross-lane reduction computes (group_sum).
+__device__ __forceinline__ int onerow_slots(int K) { return (K >> 5) <= 32 ? 32 : 64; }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of LR lanes in the tree order above; every lane of
+// a group gets the group's sum (each pair is added in both lanes, a + b ==
+// b + a).
+template <int LR>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (LR >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (LR >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (LR >= 16) v = v + dpp_f32<0x128>(v);   // row_ror:8, lane j ^ 8
+  if constexpr (LR >= 8) v = v + dpp_f32<0x141>(v);    // row_half_mirror, lane j ^ 7
+  if constexpr (LR >= 4) v = v + dpp_f32<0x4E>(v);     // quad_perm [2,3,0,1]
+  if constexpr (LR >= 2) v = v + dpp_f32<0xB1>(v);     // quad_perm [1,0,3,2]
+  return v;
+}
+
 // One decode unit: (group g, kTiles x 16 weight rows). The workgroup's
 // kDecodeWaves waves split the unit's 128-element K chunks into contiguous
 // runs (wave w takes chunks w * kChunksPerWave, ...). Every buffer load costs
@@ -535,6 +610,10 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   for (int t = 0; t < kTiles; ++t)
 #pragma unroll
     for (int s = 0; s < kAcc; ++s) acc[t][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // one row: the lane's one-row slot sums, slot 4 (wave kChunksPerWave + i)
+  // + q for the i-th chunk of each round (a round covers 32 kChunksPerWave
+  // pieces, the slot count of this K: the launch picks kChunksPerWave so)
+  float srow[kOneRow ? kTiles : 1][kChunksPerWave];
 
   // One round: this wave's chunks c0 .. c0 + kChunksPerWave - 1. All loads
   // first; in the first round the LDS staging (table, activations) happens
@@ -676,8 +755,9 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
               d[2 * (b & 1) + 1] =
                   __builtin_fmaf(w[4 * j + b][1], x[2 * (b & 1) + 1], d[2 * (b & 1) + 1]);
             }
-          acc[t][0][0] = __builtin_fmaf((d[0] + d[1]) + (d[2] + d[3]),
-                                        __uint_as_float(sb[i][t]), acc[t][0][0]);
+          const float xv = ((d[0] + d[1]) + (d[2] + d[3])) * __uint_as_float(sb[i][t]);
+          if constexpr (first) srow[t][i] = kval ? xv : 0.0f;
+          else srow[t][i] = kval ? srow[t][i] + xv : srow[t][i];
         } else if constexpr (kSplit) {
           // chunk sums of the three parts, two chains per row set
           f32x4_t c[kSets][2];
@@ -721,11 +801,17 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
 
   __syncthreads();  // the table is no longer read: its space takes the partials
   f32x4_t* s_red = reinterpret_cast<f32x4_t*>(smem);   // [kDecodeWaves][kTiles][kSetsA][64]
-  float* s_red1 = reinterpret_cast<float*>(smem);      // one row: [kDecodeWaves][kTiles][64]
+  // one row: slots [kTiles * 16][kSlots + 1], then the row sums
+  constexpr int kSlots = 32 * kChunksPerWave;
+  float* s_slot = reinterpret_cast<float*>(smem);
+  float* s_tot = s_slot + kTiles * 16 * (kSlots + 1);
+  static_assert(!kOneRow || kDecodeWaves == 8, "one-row slots assume eight waves");
 #pragma unroll
   for (int t = 0; t < kTiles; ++t) {
     if constexpr (kOneRow) {
-      s_red1[(wave * kTiles + t) * 64 + lane] = acc[t][0][0];
+#pragma unroll
+      for (int i = 0; i < kChunksPerWave; ++i)
+        s_slot[(t * 16 + nl) * (kSlots + 1) + 4 * (wave * kChunksPerWave + i) + q] = srow[t][i];
     } else {
 #pragma unroll
       for (int s = 0; s < kSetsA; ++s) {
@@ -737,18 +823,22 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
     }
   }
   __syncthreads();
+  if constexpr (kOneRow) {
+    // each row's slots through the one-row tree (64 / kSlots rows per pass)
+    constexpr int kRows = kTiles * 16, kPerPass = 64 / kSlots;
+    for (int r0w = wave * kPerPass; r0w < kRows; r0w += kDecodeWaves * kPerPass) {
+      const int r = r0w + lane / kSlots;
+      const float v = group_sum<kSlots>(s_slot[r * (kSlots + 1) + (lane % kSlots)]);
+      if (lane % kSlots == 0) s_tot[r] = v;
+    }
+    __syncthreads();
+  }
   // tile t, row set s of the output, summed over the waves in wave order;
   // NF4 lanes 0..31 add the second block's rows (lane + 32) to the first's;
-  // one row: lanes 0..15 add the four quarters of their row (element 0)
+  // one row: lanes 0..15 read their row's sum
   auto reduced = [&](int t, int s) {
     if constexpr (kOneRow) {
-      const float* r = s_red1 + t * 64 + nl;
-      constexpr int kStride = kTiles * 64;
-      float v = (r[0] + r[16]) + (r[32] + r[48]);
-#pragma unroll
-      for (int w = 1; w < kDecodeWaves; ++w)
-        v = v + ((r[w * kStride] + r[w * kStride + 16]) + (r[w * kStride + 32] + r[w * kStride + 48]));
-      return f32x4_t{v, 0.f, 0.f, 0.f};
+      return f32x4_t{s_tot[t * 16 + nl], 0.f, 0.f, 0.f};
     } else {
       const f32x4_t* r = s_red + (t * kSetsA + s) * 64 + lane;
       constexpr int kStride = kTiles * kSetsA * 64;
@@ -838,6 +928,157 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   const int g = (int)blockIdx.y;   // < G: the grid has exactly G rows of units
   decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain, kSets>(
       q, g, (int64_t)blockIdx.x, smem, lut, 0, 0, nullptr, 0u, NoWait{});
+}
+
+// A workgroup barrier for LDS only: waits for this wave's LDS operations
+// (lgkmcnt 0), not for its global loads in flight -- __syncthreads() also
+// fences global memory, which waits for every outstanding load. The empty
+// asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------------ one-row GEMV --
+//
+// k_gemv_nf4<LR, PPL, RPW>: NF4 decode where every group is one row (the
+// reference's GEMV, kernel/nf4_grouped.py:465-514), in the one-row
+// summation order above. Lanes run along the weight row: a lane owns
+// pieces j, j + LR, ... (j = lane % LR, PPL of them) of one row, so a wave
+// load of 16 bytes per lane reads 64 / LR rows of LR x 16 contiguous bytes
+// (whole cache lines), and the lane's activations (32 PPL of them) are
+// loaded once, widened to fp32 and kept in registers for every row it
+// visits. Each wave walks RPW row steps of 64 / LR rows; a workgroup of
+// eight waves covers 8 RPW (64 / LR) rows of one group (grid: row blocks x
+// groups).
+//   * The wave keeps two row steps of loads in flight and issues step s + 2
+//     before it decodes step s. Vector-memory instructions issue in order,
+//     so when the memory system pushes back the wave stalls at its next
+//     load: the codebook table is therefore built after the first two
+//     steps' loads, not after all of them, and its barrier comes early.
+//   * The pair table (as init_pair_table, 32 lane columns) is filled from
+//     immediate codebook constants: no memory load precedes it.
+//   * A row's slots are added across the LR lanes with group_sum; lane
+//     j == s of each row group keeps step s's sum, so one store per wave
+//     writes its rows' contiguous outputs.
+// Bound: HBM bytes plus one LDS lookup per packed byte (35 lane lookups
+// per ns per CU measured on MI355X). Algorithmic bytes per workgroup:
+// rows x (K / 2 + K / 16).
+template <int LR, int PPL, int RPW>
+__global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArgs p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int RS = 64 / LR;          // rows per wave step
+  constexpr int D = RPW < 2 ? RPW : 2; // row steps in flight
+  const FwdArgs q = p;
+  asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ldo));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rl = lane / LR, j = lane % LR;
+  const int g = (int)blockIdx.y;
+  // the expert id and the group's row in one round trip of scalar loads
+  const int32_t* ce = q.eids + g;
+  const int32_t* cr = q.row_off ? q.row_off + g : ce;
+  const int32_t* cr1 = q.row_off ? cr + 1 : ce;
+  int e32, ro_a, ro_b;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(ce), "s"(cr), "s"(cr1)
+      : "memory");
+  const int r0 = q.row_off ? ro_a : g;
+  if (q.row_off && ro_b - ro_a <= 0) return;   // empty group (uniform)
+  const int64_t e = e32;
+  const int K32 = (int)q.K;
+  const int PR = K32 >> 5;
+  const int N32 = (int)q.N;
+  const int wrow0 = (int)blockIdx.x * (8 * RPW * RS) + wave * (RPW * RS);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(q.a + (int64_t)r0 * q.lda, (int64_t)K32 * 2);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(q.B + e * q.sbe, q.N * q.sbn);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const char*>(q.S) + e * q.sse * 4,
+                                              q.N * q.ssn * 4);
+  // activations of the lane's pieces (64 bytes each), first in the queue
+  u32x4_t av[PPL][4];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int pc = j + i * LR;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) av[i][t] = buf_load16(ra, oob_unless(pc < PR, pc * 64 + t * 16));
+  }
+  u32x4_t wb[RPW][PPL];
+  unsigned sa[RPW][PPL];
+  auto issue = [&](int s) {
+    const int n = wrow0 + s * RS + rl;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int pc = j + i * LR;
+      const bool ok = n < N32 && pc < PR;
+      wb[s][i] = buf_load16(rb, oob_unless(ok, n * (int)q.sbn + pc * 16));
+      sa[s][i] = __builtin_amdgcn_raw_buffer_load_b32(
+          rs, oob_unless(ok, (n * (int)q.ssn + (pc >> 1)) * 4), 0, 0);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) issue(s);
+  __builtin_amdgcn_sched_barrier(0);
+  init_pair_table_imm(smem);
+  lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  // widen the activations once
+  f32x4_t af[PPL][8];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const u32x4_t x = av[i][t];
+      af[i][2 * t] = f32x4_t{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xFFFF0000u),
+                             __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xFFFF0000u)};
+      af[i][2 * t + 1] = f32x4_t{__uint_as_float(x[2] << 16), __uint_as_float(x[2] & 0xFFFF0000u),
+                                 __uint_as_float(x[3] << 16), __uint_as_float(x[3] & 0xFFFF0000u)};
+    }
+  const unsigned lane_off = (unsigned)(uintptr_t)smem | (unsigned)(lane & 31) * 8u;
+  float v[RPW];
+#pragma unroll
+  for (int s = 0; s < RPW; ++s) {
+    if (s + D < RPW) issue(s + D);
+    __builtin_amdgcn_sched_barrier(0);
+    float slot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      f32x2_t w[16];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          w[4 * jj + b] = lds_read8f(
+              __builtin_amdgcn_perm(wb[s][i][jj], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
+      float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const f32x4_t& x = af[i][2 * jj + (b >> 1)];
+          d[2 * (b & 1)] = __builtin_fmaf(w[4 * jj + b][0], x[2 * (b & 1)], d[2 * (b & 1)]);
+          d[2 * (b & 1) + 1] =
+              __builtin_fmaf(w[4 * jj + b][1], x[2 * (b & 1) + 1], d[2 * (b & 1) + 1]);
+        }
+      const float xv = ((d[0] + d[1]) + (d[2] + d[3])) * __uint_as_float(sa[s][i]);
+      const bool valid = j + i * LR < PR;
+      if (i == 0) slot = valid ? xv : 0.0f;
+      else slot = valid ? slot + xv : slot;
+    }
+    v[s] = group_sum<LR>(slot);
+  }
+  float ov = v[0];
+#pragma unroll
+  for (int s = 1; s < RPW; ++s) ov = j == s ? v[s] : ov;
+  const int n = wrow0 + j * RS + rl;
+  if (j < RPW && n < N32) q.out[(int64_t)r0 * q.ldo + n] = f32_to_bf16_bits(ov);
 }
 
 // ------------------------------------------------- row-streaming decode --
@@ -1119,17 +1360,6 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
     }
   // the ring's last refills (past the end: zero-size offsets) are in flight
   __builtin_amdgcn_s_waitcnt(0);
-}
-
-// A workgroup barrier for LDS only: waits for this wave's LDS operations
-// (lgkmcnt 0), not for its global loads in flight -- __syncthreads() also
-// fences global memory, which waits for every outstanding load. The empty
-// asm statements keep the compiler from moving memory accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0) only
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
 }
 
 // ------------------------------------------------- unit-streaming decode --
@@ -3255,6 +3485,53 @@ int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream)
   return 0;
 }
 
+// One-row NF4 decode launch (k_gemv_nf4): every group exactly one row and
+// K <= 8192 (at most four pieces per lane). Row steps per wave: enough for
+// one workgroup per CU over the launch's rows, at most six (Qwen3-30B-A3B
+// batch 1: gate_up 6, down 4; measured on MI355X against 3 and 12 per wave,
+// and 1024-thread workgroups: no faster). Returns 1 when the launch is not
+// for it.
+template <int LR, int PPL, int RPW>
+int launch_gemv_inst(const FwdArgs& p, hipStream_t stream) {
+  const int64_t rows_wg = 8 * RPW * (64 / LR);
+  const int64_t gx = (p.N + rows_wg - 1) / rows_wg;
+  if (gx > 0x7FFFFFFF) return -1;
+  hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW>), dim3((unsigned)gx, (unsigned)p.G, 1), dim3(512),
+                     8 * kPairEntries, stream, p);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+template <int LR, int PPL>
+int launch_gemv_rpw(const FwdArgs& p, int rpw, hipStream_t stream) {
+  switch (rpw) {
+    case 2: return launch_gemv_inst<LR, PPL, 2>(p, stream);
+    case 4: return launch_gemv_inst<LR, PPL, 4>(p, stream);
+    default: return launch_gemv_inst<LR, PPL, 6>(p, stream);
+  }
+}
+
+int launch_gemv(const FwdArgs& p, hipStream_t stream) {
+  if (p.K <= 0 || p.K % 64 != 0 || p.N <= 0 || p.G <= 0) return 1;
+  const int64_t pr = p.K / 32;
+  const int lr = pr <= 32 ? 32 : 64;
+  const int64_t ppl = (pr + lr - 1) / lr;
+  if (ppl > 4) return 1;
+  // 32-bit row offsets inside the expert's resources
+  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * 4 > 0x7FFFFFFF) return 1;
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  const int64_t per_step = (int64_t)cus * 8 * (64 / lr);   // rows of one row step, all CUs
+  const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
+  const int rpw = want <= 2 ? 2 : want <= 4 ? 4 : 6;
+  if (lr == 32) return launch_gemv_rpw<32, 1>(p, rpw, stream);
+  switch (ppl) {
+    case 1: return launch_gemv_rpw<64, 1>(p, rpw, stream);
+    case 2: return launch_gemv_rpw<64, 2>(p, rpw, stream);
+    case 3: return launch_gemv_rpw<64, 3>(p, rpw, stream);
+    default: return launch_gemv_rpw<64, 4>(p, rpw, stream);
+  }
+}
+
 // pa: LDS-staged activation pieces per thread (0: register operands);
 // sets: NF4 row sets (0: one-row groups on the fp32 FMA path, 2 when a group
 // has more than 8 rows)
@@ -3320,6 +3597,10 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   const int pa = decode_stage<FMT>(p.K, p.max_m, &a_bytes);
   const bool stage = pa > 0;
   const int sets = FMT != kNF4 ? 1 : p.max_m > 8 ? 2 : (p.max_m == 1 && pa > 0) ? 0 : 1;
+  if (FMT == kNF4 && sets == 0) {   // one-row groups: the row-major GEMV, same bits
+    const int rc = launch_gemv(p, stream);
+    if (rc <= 0) return rc;
+  }
   const int64_t red = (int64_t)kW * kT * (sets > 0 ? sets : 1) * 64 * 16;
   const int64_t table = FMT == kNF4 ? kSplitTabBytes : 0;
   int64_t lds = table + kDecodeFlagBytes + (stage ? a_bytes : 0) + 64;

@@ -20,6 +20,8 @@ Also reported:
                forms, a whole device-routed decode MoE layer (top-k ->
                grouping -> gather -> FFN -> combine, one graph), GPT-OSS-20B MXFP4 decode, Qwen3 NF4 Zipf prefill and
                down-projection dgrad TFLOP/s.
+  floor        per launch, an empty launch and a plain read of the same
+               bytes (csrc/gnf4_floor.hip), next to the roofline.
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -283,6 +285,89 @@ def ffn_report(model):
     return r
 
 
+def _floor_lib():
+    """The measurement kernels of grouped-nf4-gemm_amd/csrc/gnf4_floor.hip."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "grouped-nf4-gemm_amd" / "libgnf4_floor.so"))
+    lib.gnf4_floor_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.gnf4_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
+def _graph_us(run, launches, dev, replays=20):
+    """Average time (us) per launch of run() (which makes `launches`
+    launches), captured once as a graph and replayed, HIP events on the
+    launch stream."""
+    import torch
+    _, graph = time_graph(run, 1, 2, dev, settle=True)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (replays * launches)
+
+
+def floor_report(m, which="gu"):
+    """What a decode launch of this shape can reach, measured like the
+    decode kernels (a graph of every layer's launches): an empty launch of
+    256 workgroups, and a plain 16-byte-per-lane read of exactly the active
+    experts' packed bytes (each layer's own buffer, expert ids from a device
+    table) that computes nothing. Returns per-launch times and rates."""
+    import torch
+    lib = _floor_lib()
+    W = [w[0] for w in (m.gu if which == "gu" else m.dn)]
+    sink = torch.zeros(1, dtype=torch.int32, device=m.dev)
+    region = W[0].shape[1] * W[0].stride(1)
+
+    def run_empty():
+        stream = torch.cuda.current_stream(m.dev).cuda_stream   # the capturing stream
+        for _ in range(m.L):
+            assert lib.gnf4_floor_empty(256, 1, stream) == 0
+
+    def run_read():
+        stream = torch.cuda.current_stream(m.dev).cuda_stream
+        for l in range(m.L):
+            eids = m.routes[l][1]
+            assert lib.gnf4_floor_read(W[l].data_ptr(), W[l].stride(0), region, eids.data_ptr(),
+                                       eids.numel(), sink.data_ptr(), stream) == 0
+
+    empty = _graph_us(run_empty, m.L, m.dev)
+    read = _graph_us(run_read, m.L, m.dev)
+    nbytes = sum(m.bytes_gu if which == "gu" else m.bytes_dn) / m.L
+    return {"empty_launch_us": round(empty, 3), "plain_read_us": round(read, 3),
+            "plain_read_gbs": round(nbytes / (read * 1e-6) / 1e9, 1),
+            "plain_read_frac": round(nbytes / (read * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def floor_workload(dev):
+    """bench.py --floor: per-launch floors next to the decode kernels at batch
+    1, Qwen3 NF4 gate_up / down and GPT-OSS-20B MXFP4 gate_up / down, every
+    model layer its own weights (48 x 12.6 MB and 24 x 33 MB per gate_up
+    graph: far more than the 256 MB Infinity Cache)."""
+    out = {}
+    for name, fmt, cfg in (("qwen3_nf4", "nf4", QWEN), ("gptoss_mxfp4", "mxfp4", GPTOSS)):
+        L = cfg["layers"]
+        m = DecodeModel(fmt, cfg, 1, dev, layers=L)
+        for which in ("gu", "dn"):
+            f = floor_report(m, which)
+            k_us = m.kernel_ms(which) * 1e3
+            nbytes = sum(m.bytes_gu if which == "gu" else m.bytes_dn) / m.L
+            f["kernel_us"] = round(k_us, 3)
+            f["kernel_gbs"] = round(nbytes / (k_us * 1e-6) / 1e9, 1)
+            f["kernel_frac"] = round(f["kernel_gbs"] / HBM_PEAK_GBS, 4)
+            f["packed_bytes_per_launch"] = int(nbytes)
+            out[f"{name}_{'gate_up' if which == 'gu' else 'down'}_b1"] = f
+            log(f"[bench] floor {name} {which}: {json.dumps(f)}")
+        del m
+        import torch
+        torch.cuda.empty_cache()
+    return out
+
+
 def decode_report(m):
     """Per-launch rates of one decode configuration: gate_up and down packed
     GB/s (graph of every layer's launches, HIP events), active experts per
@@ -539,6 +624,9 @@ def main():
                          "launched eagerly twice; prints nothing else")
     ap.add_argument("--fmt", choices=("nf4", "mxfp4"), default="nf4",
                     help="with --pmc-workload: Qwen3 NF4 (default) or GPT-OSS-20B MXFP4 experts")
+    ap.add_argument("--floor", action="store_true",
+                    help="batch-1 decode launches next to their floors (an empty launch and a "
+                         "plain read of the same bytes), Qwen3 NF4 and GPT-OSS MXFP4; one JSON line")
     ap.add_argument("--pmc-prefill-workload", action="store_true",
                     help="for rocprofv3 --pmc: the 256 MiB copy, then config 4's prefill "
                          "gate_up and down calls, three each")
@@ -553,6 +641,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_prefill_workload:
         pmc_prefill_workload(dev)
+        return
+    if args.floor:
+        print(json.dumps({"floor": floor_workload(dev)}), flush=True)
         return
     if args.mma_workload:
         log(f"[bench] prefill {json.dumps(prefill_tflops(dev))}")
@@ -579,26 +670,32 @@ def main():
     log(f"[bench] gate_up decode kernel {avg_ms * 1e3:.2f} us -> {achieved:.1f} GB/s; "
         f"down {dn_ms * 1e3:.2f} us -> {dn_gbs:.1f} GB/s")
 
-    extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1)}}
+    floor_gu, floor_dn = floor_report(model, "gu"), floor_report(model, "dn")
+    log(f"[bench] floors: gate_up {json.dumps(floor_gu)}, down {json.dumps(floor_dn)}")
+    extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1),
+                             "floor": floor_dn}}
     extra[f"qwen3_nf4_ffn_b{args.batch}"] = ffn_report(model)
     log(f"[bench] ffn: {json.dumps(extra[f'qwen3_nf4_ffn_b{args.batch}'])}")
     extra["qwen3_nf4_decode_b1_eager_op_us"] = round(model.eager_us(), 2)
     if not args.no_extra:
-        # config 2's batch sweep on 16 of the model's layers (their own bytes)
+        # config 2's batch sweep over the model's layers (their own bytes: at
+        # batch 1 a graph of fewer layers could sit in the 256 MB Infinity Cache)
         sweep = {}
         for b in (1, 4, 16):
-            m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=16, weights=(model.gu, model.dn))
+            m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=model.L, weights=(model.gu, model.dn))
             sweep[f"b{b}"] = decode_report(m)
             if b > 1:
                 extra[f"qwen3_nf4_ffn_b{b}"] = ffn_report(m)
             del m
         extra["qwen3_nf4_decode_sweep"] = sweep
-        # config 3's batch sweep, GPT-OSS-20B MXFP4 experts (6 layers' own bytes)
-        mx = (make_mx_layers(GPTOSS["E"], *GPTOSS["gu"], 6, dev, 100),
-              make_mx_layers(GPTOSS["E"], *GPTOSS["dn"], 6, dev, 101))
+        # config 3's batch sweep, GPT-OSS-20B MXFP4 experts (all 24 layers'
+        # own bytes, 33 MB per gate_up launch at batch 1)
+        L_mx = GPTOSS["layers"]
+        mx = (make_mx_layers(GPTOSS["E"], *GPTOSS["gu"], L_mx, dev, 100),
+              make_mx_layers(GPTOSS["E"], *GPTOSS["dn"], L_mx, dev, 101))
         sweep = {}
         for b in (1, 2, 4, 8, 16, 32, 64):
-            m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=6, weights=mx)
+            m = DecodeModel("mxfp4", GPTOSS, b, dev, seed=100 + b, layers=L_mx, weights=mx)
             sweep[f"b{b}"] = decode_report(m)
             del m
         extra["gptoss20b_mxfp4_decode_sweep"] = sweep
@@ -638,7 +735,11 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
                      "kernel": "k_decode_fwd<NF4> (gate_up, 8 experts x 1536 x 1024 B per launch)",
                      "avg_launch_us": round(avg_ms * 1e3, 3),
-                     "timing": "HIP events around 20 replays of a graph of 48 back-to-back launches"},
+                     "timing": "HIP events around 20 replays of a graph of 48 back-to-back launches",
+                     "floor": dict(floor_gu, note="same launch shape and bytes, nothing computed: "
+                                   "an empty launch and a plain 16-byte-per-lane read of the "
+                                   "active experts' packed bytes (grouped-nf4-gemm_amd/csrc/"
+                                   "gnf4_floor.hip), timed like the kernel")},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -2,7 +2,8 @@
 
 ``python build.py`` (or ``build()``) compiles the HIP sources in csrc/ (the
 grouped GEMM kernels and the routing kernels) into ``libgnf4_hip.so`` next to
-this file. It always recompiles: the library must
+this file, and the measurement kernels bench.py times against
+(``csrc/gnf4_floor.hip``) into ``libgnf4_floor.so``. It always recompiles: the library must
 track its source, and the GPU box only ever loads the prebuilt file.
 """
 from __future__ import annotations
@@ -15,6 +16,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 SRCS = [HERE / "csrc" / "gnf4_hip.hip", HERE / "csrc" / "gnf4_route.hip"]
 OUT = HERE / "libgnf4_hip.so"
+FLOOR_SRCS = [HERE / "csrc" / "gnf4_floor.hip"]
+FLOOR_OUT = HERE / "libgnf4_floor.so"
 ARCH = os.environ.get("GNF4_HIP_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32 for
@@ -33,9 +36,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC)")
 
 
-def build(verbose: bool = False) -> Path:
-    tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), *(str(p) for p in SRCS)]
+def _compile(srcs, out: Path, verbose: bool) -> Path:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, "-o", str(tmp), *(str(p) for p in srcs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so.
     noise = "is not a recognized feature for this target"
@@ -44,8 +47,13 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{msgs}")
     if verbose and msgs.strip():
         print(msgs)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
+
+
+def build(verbose: bool = False) -> Path:
+    _compile(FLOOR_SRCS, FLOOR_OUT, verbose)
+    return _compile(SRCS, OUT, verbose)
 
 
 if __name__ == "__main__":

@@ -1081,6 +1081,111 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   if (j < RPW && n < N32) q.out[(int64_t)r0 * q.ldo + n] = f32_to_bf16_bits(ov);
 }
 
+// k_gemv_mx<LR, PPL, RPW>: the same row-major walk for MXFP4 groups of one
+// row (reference kernel/mxfp4_grouped.py:100-131). A 16-byte piece is one
+// e8m0 scale block; v_cvt_scalef32_pk_bf16_fp4 turns each packed byte into
+// a bf16 pair already scaled by 2^(e - 127) (exact), and v_dot2_f32_bf16
+// multiplies it with the activation pair and adds it into one of four fp32
+// chains. No table, so no LDS and no barrier: the wave issues its first two
+// row steps and starts on the first as soon as it lands.
+// One-row MXFP4 order: piece p: h_p = (d0 + d1) + (d2 + d3), chain c taking
+// the dot of byte 4 j + c for j = 0..3 in order; slots and tree as the NF4
+// one-row order, with LR chosen per K by the launch (mx_slots).
+// (The activation pairs are taken out of a bf16x8 view of each 16-byte
+// chunk by element shuffles: hipcc 7.2 folds a bit_cast of dword 1..3 of a
+// u32x4 into a bf16x2 to dword 0.)
+template <int LR, int PPL, int RPW>
+__global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p) {
+  constexpr int RS = 64 / LR;
+  constexpr int D = RPW < 2 ? RPW : 2;
+  const FwdArgs q = p;
+  asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ldo));
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rl = lane / LR, j = lane % LR;
+  const int g = (int)blockIdx.y;
+  const int32_t* ce = q.eids + g;
+  const int32_t* cr = q.row_off ? q.row_off + g : ce;
+  const int32_t* cr1 = q.row_off ? cr + 1 : ce;
+  int e32, ro_a, ro_b;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+      : "s"(ce), "s"(cr), "s"(cr1)
+      : "memory");
+  const int r0 = q.row_off ? ro_a : g;
+  if (q.row_off && ro_b - ro_a <= 0) return;   // empty group (uniform)
+  const int64_t e = e32;
+  const int K32 = (int)q.K;
+  const int PR = K32 >> 5;
+  const int N32 = (int)q.N;
+  const int wrow0 = (int)blockIdx.x * (8 * RPW * RS) + wave * (RPW * RS);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(q.a + (int64_t)r0 * q.lda, (int64_t)K32 * 2);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(q.B + e * q.sbe, q.N * q.sbn);
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(static_cast<const uint8_t*>(q.S) + e * q.sse, q.N * q.ssn);
+  u32x4_t av[PPL][4];
+#pragma unroll
+  for (int i = 0; i < PPL; ++i) {
+    const int pc = j + i * LR;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) av[i][t] = buf_load16(ra, oob_unless(pc < PR, pc * 64 + t * 16));
+  }
+  u32x4_t wb[RPW][PPL];
+  unsigned sb[RPW][PPL];
+  auto issue = [&](int s) {
+    const int n = wrow0 + s * RS + rl;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const int pc = j + i * LR;
+      const bool ok = n < N32 && pc < PR;
+      wb[s][i] = buf_load16(rb, oob_unless(ok, n * (int)q.sbn + pc * 16));
+      sb[s][i] = buf_load1(rs, oob_unless(ok, n * (int)q.ssn + pc));
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < D; ++s) issue(s);
+  float v[RPW];
+#pragma unroll
+  for (int s = 0; s < RPW; ++s) {
+    if (s + D < RPW) issue(s + D);
+    __builtin_amdgcn_sched_barrier(0);
+    float slot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PPL; ++i) {
+      const float sc = e8m0_to_f32(sb[s][i]);
+      float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const unsigned x = wb[s][i][jj];
+        const bf16x8_t a8 = as_bf16x8(av[i][jj]);
+        d[0] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 0),
+                                               __builtin_shufflevector(a8, a8, 0, 1), d[0], false);
+        d[1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 1),
+                                               __builtin_shufflevector(a8, a8, 2, 3), d[1], false);
+        d[2] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 2),
+                                               __builtin_shufflevector(a8, a8, 4, 5), d[2], false);
+        d[3] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(x, sc, 3),
+                                               __builtin_shufflevector(a8, a8, 6, 7), d[3], false);
+      }
+      const float xv = (d[0] + d[1]) + (d[2] + d[3]);
+      const bool valid = j + i * LR < PR;
+      if (i == 0) slot = valid ? xv : 0.0f;
+      else slot = valid ? slot + xv : slot;
+    }
+    v[s] = group_sum<LR>(slot);
+  }
+  float ov = v[0];
+#pragma unroll
+  for (int s = 1; s < RPW; ++s) ov = j == s ? v[s] : ov;
+  const int n = wrow0 + j * RS + rl;
+  if (j < RPW && n < N32) q.out[(int64_t)r0 * q.ldo + n] = f32_to_bf16_bits(ov);
+}
+
 // ------------------------------------------------- row-streaming decode --
 //
 // k_decode_rows<FMT, kW, kT, kSets, kCpw, kR, kP, kAbsBlock>: decode (every group <= 16
@@ -3485,50 +3590,75 @@ int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream)
   return 0;
 }
 
-// One-row NF4 decode launch (k_gemv_nf4): every group exactly one row and
-// K <= 8192 (at most four pieces per lane). Row steps per wave: enough for
-// one workgroup per CU over the launch's rows, at most six (Qwen3-30B-A3B
-// batch 1: gate_up 6, down 4; measured on MI355X against 3 and 12 per wave,
-// and 1024-thread workgroups: no faster). Returns 1 when the launch is not
-// for it.
-template <int LR, int PPL, int RPW>
+// One-row decode launch (k_gemv_nf4, k_gemv_mx): every group exactly one
+// row and at most four pieces per lane (NF4 K <= 8192). Row steps per wave:
+// enough for about one workgroup per CU over the launch's rows, at most six
+// (measured on MI355X at batch 1: Qwen3-30B-A3B gate_up 6 and down 4,
+// GPT-OSS-20B gate_up 6 and down 3 per wave were the fastest of 1..12;
+// more, smaller workgroups and 1024-thread workgroups were slower). Returns
+// 1 when the launch is not for it.
+template <int FMT, int LR, int PPL, int RPW>
 int launch_gemv_inst(const FwdArgs& p, hipStream_t stream) {
   const int64_t rows_wg = 8 * RPW * (64 / LR);
   const int64_t gx = (p.N + rows_wg - 1) / rows_wg;
   if (gx > 0x7FFFFFFF) return -1;
-  hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW>), dim3((unsigned)gx, (unsigned)p.G, 1), dim3(512),
-                     8 * kPairEntries, stream, p);
+  const dim3 grid((unsigned)gx, (unsigned)p.G, 1);
+  if constexpr (FMT == kNF4)
+    hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW>), grid, dim3(512), 8 * kPairEntries, stream, p);
+  else
+    hipLaunchKernelGGL((k_gemv_mx<LR, PPL, RPW>), grid, dim3(512), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-template <int LR, int PPL>
+template <int FMT, int LR, int PPL>
 int launch_gemv_rpw(const FwdArgs& p, int rpw, hipStream_t stream) {
   switch (rpw) {
-    case 2: return launch_gemv_inst<LR, PPL, 2>(p, stream);
-    case 4: return launch_gemv_inst<LR, PPL, 4>(p, stream);
-    default: return launch_gemv_inst<LR, PPL, 6>(p, stream);
+    case 2: return launch_gemv_inst<FMT, LR, PPL, 2>(p, stream);
+    case 3: return launch_gemv_inst<FMT, LR, PPL, 3>(p, stream);
+    case 4: return launch_gemv_inst<FMT, LR, PPL, 4>(p, stream);
+    default: return launch_gemv_inst<FMT, LR, PPL, 6>(p, stream);
   }
 }
 
+// Slots per row of the one-row order: NF4 follows onerow_slots (the fused
+// FFN's decode units share it); MXFP4 takes whichever of 32 and 64 leaves
+// fewer idle lanes (GPT-OSS-20B K = 2880: 90 pieces, 3 x 32 lanes).
+template <int FMT>
+int gemv_slots(int64_t pr) {
+  if (FMT == kNF4) return pr <= 32 ? 32 : 64;
+  return 32 * ((pr + 31) / 32) < 64 * ((pr + 63) / 64) ? 32 : 64;
+}
+
+template <int FMT>
 int launch_gemv(const FwdArgs& p, hipStream_t stream) {
-  if (p.K <= 0 || p.K % 64 != 0 || p.N <= 0 || p.G <= 0) return 1;
+  if (p.K <= 0 || p.K % (FMT == kNF4 ? 64 : 32) != 0 || p.N <= 0 || p.G <= 0) return 1;
   const int64_t pr = p.K / 32;
-  const int lr = pr <= 32 ? 32 : 64;
+  const int lr = gemv_slots<FMT>(pr);
   const int64_t ppl = (pr + lr - 1) / lr;
   if (ppl > 4) return 1;
   // 32-bit row offsets inside the expert's resources
-  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * 4 > 0x7FFFFFFF) return 1;
+  const int64_t sbytes = FMT == kNF4 ? 4 : 1;
+  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * sbytes > 0x7FFFFFFF) return 1;
   const int cus = device_cus();
   if (cus <= 0) return -2;
-  const int64_t per_step = (int64_t)cus * 8 * (64 / lr);   // rows of one row step, all CUs
+  // row steps per wave: about one workgroup per CU over the launch's rows
+  const int64_t per_step = (int64_t)cus * 8 * (64 / lr);
   const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
-  const int rpw = want <= 2 ? 2 : want <= 4 ? 4 : 6;
-  if (lr == 32) return launch_gemv_rpw<32, 1>(p, rpw, stream);
+  const int rpw = want <= 2 ? 2 : want <= 3 ? 3 : want <= 4 ? 4 : 6;
+  if (lr == 32) {
+    if constexpr (FMT == kNF4) return launch_gemv_rpw<FMT, 32, 1>(p, rpw, stream);   // pr <= 32
+    switch (ppl) {
+      case 1: return launch_gemv_rpw<FMT, 32, 1>(p, rpw, stream);
+      case 2: return launch_gemv_rpw<FMT, 32, 2>(p, rpw, stream);
+      case 3: return launch_gemv_rpw<FMT, 32, 3>(p, rpw, stream);
+      default: return launch_gemv_rpw<FMT, 32, 4>(p, rpw, stream);
+    }
+  }
   switch (ppl) {
-    case 1: return launch_gemv_rpw<64, 1>(p, rpw, stream);
-    case 2: return launch_gemv_rpw<64, 2>(p, rpw, stream);
-    case 3: return launch_gemv_rpw<64, 3>(p, rpw, stream);
-    default: return launch_gemv_rpw<64, 4>(p, rpw, stream);
+    case 1: return launch_gemv_rpw<FMT, 64, 1>(p, rpw, stream);
+    case 2: return launch_gemv_rpw<FMT, 64, 2>(p, rpw, stream);
+    case 3: return launch_gemv_rpw<FMT, 64, 3>(p, rpw, stream);
+    default: return launch_gemv_rpw<FMT, 64, 4>(p, rpw, stream);
   }
 }
 
@@ -3597,8 +3727,10 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   const int pa = decode_stage<FMT>(p.K, p.max_m, &a_bytes);
   const bool stage = pa > 0;
   const int sets = FMT != kNF4 ? 1 : p.max_m > 8 ? 2 : (p.max_m == 1 && pa > 0) ? 0 : 1;
-  if (FMT == kNF4 && sets == 0) {   // one-row groups: the row-major GEMV, same bits
-    const int rc = launch_gemv(p, stream);
+  if ((FMT == kNF4 && sets == 0) || (FMT == kMX && p.max_m == 1)) {
+    // one-row groups: the row-major GEMV (NF4: same bits as decode_unit's
+    // one-row form)
+    const int rc = launch_gemv<FMT>(p, stream);
     if (rc <= 0) return rc;
   }
   const int64_t red = (int64_t)kW * kT * (sets > 0 ? sets : 1) * 64 * 16;

@@ -448,9 +448,9 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
     """A group's decoded rows are the same bits in a launch of many units as
     in a launch of that group with only the batch's largest group beside it,
     and the whole meets the contract. The largest group fixes the launch's
-    class (NF4: one row, up to 8 rows, 9..16 rows: the arithmetic and the
-    chunks per wave differ between classes); within a class no group's bits
-    depend on the others. Covers ragged groups, empty groups, a K tail
+    class (NF4: one row, up to 8 rows, 9..16 rows; MXFP4: one row, more
+    rows: the arithmetic and the chunks per wave differ between classes);
+    within a class no group's bits depend on the others. Covers ragged groups, empty groups, a K tail
     (2880 = 22.5 chunks) and N past a 128-row boundary."""
     E = 24
     W, S = _stack(fmt, E, N, K, seed=31)
@@ -485,7 +485,7 @@ def test_decode_group_rows_do_not_depend_on_the_batch(fmt, N, K):
                                             ("mxfp4", 1560, 2880, 4, 20)])
 def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows, G):
     """Batched launches (20..86 groups) run the unit walks -- MXFP4 at
-    K = 2880 (1..16 rows; 20 groups: walks of 5 units), NF4 at
+    K = 2880 (2..16 rows; 20 groups: walks of 5 units), NF4 at
     1024 < K <= 2048 (2..8 rows); a launch of
     one or two groups runs the per-unit kernel. Both must give the same bits
     for every group (NF4: all of them; same chunk split per wave, same
@@ -507,10 +507,11 @@ def test_streamed_decode_matches_the_per_unit_kernel(fmt, N, K, rows, G):
         r0, m = sum(sizes[:gi]), sizes[gi]
         if m == 0:
             continue
-        # one group alone (NF4: beside a group of the batch's largest size,
-        # which keeps the launch class; two groups still take the per-unit
-        # kernel at these shapes)
-        pad = rows if fmt == "nf4" and m < rows else 0
+        # one group alone, beside a group of the batch's largest size, which
+        # keeps the launch class (a launch of one-row groups takes the
+        # one-row GEMV, in either format); two groups still take the
+        # per-unit kernel at these shapes
+        pad = rows if m < rows else 0
         aa = torch.cat([a[r0:r0 + m], a[:pad]]) if pad else a[r0:r0 + m]
         alone = op(aa, W, S, [m] + ([pad] if pad else []), [ids[gi]] + ([ids[gi]] if pad else []))
         assert torch.equal(out[r0:r0 + m], alone[:m]), f"group {gi} differs"

@@ -4242,11 +4242,25 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 // Sync words of gnf4_hip_nf4_ffn_fwd_noalloc: a fixed device array per GPU
 // (each device that loads this library holds its own copy until the process
 // ends), so that entry point allocates nothing. Zero at load; every call
-// leaves its flags zero again and a flag left behind by a timed-out call
-// carries an older epoch, so nothing has to be cleared between calls. Word 0
-// is the sticky error word (its time-out also writes NaN outputs). Calls
-// that overlap on one GPU share the array and race.
+// that completes leaves its flags zero again. A down unit that times out
+// sets word 0 (the sticky error word) and writes NaN, and the gate/up units
+// that finish after it leave their flags set to that call's epoch. An eager
+// call after that is still exact (it has a new epoch), but a captured graph
+// replays its launch with the same epoch, so its next replay could accept
+// those flags before its own h is written: after a time-out, run
+// gnf4_hip_nf4_ffn_noalloc_reset (stream-ordered, no allocation) before any
+// further replay. Calls that overlap on one GPU share the array and race.
 constexpr int64_t kFfnScratchWords = int64_t(1) << 19;   // 2 MiB
+
+// Copies word 0 (the error word) to *err (when err is not null) and clears
+// all n words: block 0 reads word 0 before its own threads clear it.
+__global__ void __launch_bounds__(256) k_ffn_scratch_reset(uint32_t* __restrict__ words, int64_t n,
+                                                           uint32_t* __restrict__ err) {
+  const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i0 == 0 && err) *err = words[0];
+  __syncthreads();
+  for (int64_t i = i0; i < n; i += (int64_t)gridDim.x * blockDim.x) words[i] = 0u;
+}
 
 }  // namespace
 
@@ -4438,6 +4452,14 @@ int gnf4_hip_nf4_ffn_fwd_noalloc(const void* a, int a_dtype, int64_t lda, const 
                               B_dn, dn_sbe, dn_sbn, absmax_dn, dn_sae, dn_san, expert_ids,
                               row_off, G, max_m, N_gu, K, N_dn, h, ldh, words,
                               kFfnScratchWords, out, ldo, stream);
+}
+
+int gnf4_hip_nf4_ffn_noalloc_reset(uint32_t* error_word, void* stream) {
+  uint32_t* words = ffn_scratch_words();
+  if (!words) return -2;
+  hipLaunchKernelGGL(k_ffn_scratch_reset, dim3(256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), words, kFfnScratchWords, error_word);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 7
+#define GNF4_HIP_ABI_VERSION 8
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -196,8 +196,11 @@ int gnf4_hip_nf4_ffn_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t 
  * array's size), otherwise what gnf4_hip_nf4_ffn_fwd returns. Every call on
  * a GPU shares that GPU's array: calls that overlap on one GPU race (run
  * them in one stream order). A down unit that times out writes NaN into
- * its output rows; the array's error word is not readable through this
- * ABI. */
+ * its output rows and sets the array's error word; read and clear it with
+ * gnf4_hip_nf4_ffn_noalloc_reset. Under graph capture the call's epoch is
+ * fixed in the graph: after a replay that timed out, run the reset before
+ * replaying again (otherwise flags left by that replay's late gate/up units
+ * could pass the next replay's down units early). */
 int gnf4_hip_nf4_ffn_fwd_noalloc(const void *a, int a_dtype, int64_t lda,
                                  const uint8_t *B_gu, int64_t gu_sbe, int64_t gu_sbn,
                                  const float *absmax_gu, int64_t gu_sae, int64_t gu_san,
@@ -206,6 +209,16 @@ int gnf4_hip_nf4_ffn_fwd_noalloc(const void *a, int a_dtype, int64_t lda,
                                  const int32_t *expert_ids, const int32_t *row_off, int G,
                                  int max_m, int64_t N_gu, int64_t K, int64_t N_dn, void *h,
                                  int64_t ldh, void *out, int64_t ldo, void *stream);
+
+/* Stream-ordered read and clear of the fixed sync array of
+ * gnf4_hip_nf4_ffn_fwd_noalloc on the current device: copies its error word
+ * (nonzero when a down unit of an earlier call timed out) to *error_word
+ * (device memory, or pinned host memory at its device address; may be
+ * NULL), then zeroes the whole array with a kernel (no hipMemsetAsync, so
+ * it can be captured in a graph). Allocates nothing. No counterpart in the
+ * reference; for the same callers as the no-allocation entry point. 0 on
+ * success, -2 on a runtime error. */
+int gnf4_hip_nf4_ffn_noalloc_reset(uint32_t *error_word, void *stream);
 
 /* Grouped dgrad for either format: out[t, :] = grad_out[t, :] . dequant(W[e(t)]),
  * contracting over N in fixed 64-wide ascending steps (output bits do not

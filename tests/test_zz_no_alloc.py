@@ -106,3 +106,69 @@ def test_noalloc_rejects_sizes_beyond_its_array():
                                           p, p, G, 1, N_gu, 2048, N_dn, p, 1536, p, 2048,
                                           torch.cuda.current_stream().cuda_stream)
     assert rc == -1
+
+
+def _reset(lib):
+    err = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    assert lib.gnf4_hip_nf4_ffn_noalloc_reset(err.data_ptr(),
+                                              torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    return int(err.item())
+
+
+def test_noalloc_reset_after_forced_time_outs_in_a_captured_graph():
+    """A spin limit of 0 polls (forced from the host: a down unit that does
+    not find its h ready at once gives up, and every kernel still exits) on
+    a captured no-allocation call. Each replay's down units give either the
+    allocating entry point's bits or NaN; the reset reports the error word
+    exactly when some output is NaN and clears the array (flags the late
+    gate/up units left included). A graph captured after it, with the normal
+    limit, then replays exact, three times in a row."""
+    lib = _lib()
+    E, H, K, N_dn = 32, 512, 1024, 1024
+    sizes, ids = [1, 3, 2, 4, 1, 1, 2, 2], [3, 7, 11, 15, 19, 23, 27, 31]
+    prob = _problem(E, H, K, N_dn, sizes, ids, 95)
+    want, _ = _run(False, prob, sizes)
+    assert _reset(lib) == 0
+    a = prob[0]
+    T = a.shape[0]
+    h = torch.empty(T, H, dtype=torch.bfloat16, device=a.device)
+    out = torch.empty(T, N_dn, dtype=torch.bfloat16, device=a.device)
+
+    def call():
+        head, tail = _args(*prob, len(sizes), max(sizes), h, out)
+        assert lib.gnf4_hip_nf4_ffn_fwd_noalloc(*head, *tail) == 0
+
+    try:
+        assert lib.gnf4_hip_ffn_set_spin_limit(0) == 0
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            call()
+    finally:
+        assert lib.gnf4_hip_ffn_set_spin_limit(1 << 22) == 0
+    for _ in range(3):
+        out.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        nan = torch.isnan(out.float())
+        row0 = 0
+        for m in sizes:
+            for c0 in range(0, N_dn, 32):
+                blk = nan[row0:row0 + m, c0:c0 + 32]
+                assert bool(blk.all()) or not bool(blk.any())
+                if not bool(blk.any()):
+                    assert torch.equal(out[row0:row0 + m, c0:c0 + 32].view(torch.int16),
+                                       want[row0:row0 + m, c0:c0 + 32].view(torch.int16))
+            row0 += m
+        assert (_reset(lib) != 0) == bool(nan.any())
+    assert _reset(lib) == 0
+    del g
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        call()
+    for _ in range(3):
+        out.fill_(7.0)
+        g2.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert _reset(lib) == 0

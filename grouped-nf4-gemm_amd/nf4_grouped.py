@@ -288,14 +288,25 @@ class _TableRing:
 _ARENAS: dict = {}
 _RINGS: dict = {}
 _TABLE_RINGS: dict = {}
+# Creation of the per-device arenas and per-(device, stream) rings: two
+# threads making their first call on one stream must get the same ring (a
+# dropped ring's pinned block could be reused while a kernel still reads
+# group tables from it). Rings are never freed.
+_REGISTRY_LOCK = threading.Lock()
+
+
+def _registered(table, key, make):
+    obj = table.get(key)
+    if obj is None:
+        with _REGISTRY_LOCK:
+            obj = table.get(key)
+            if obj is None:
+                obj = table[key] = make()
+    return obj
 
 
 def _table_ring(dev, stream) -> _TableRing:
-    key = (str(dev), stream.cuda_stream)
-    ring = _TABLE_RINGS.get(key)
-    if ring is None:
-        ring = _TABLE_RINGS[key] = _TableRing(dev)
-    return ring
+    return _registered(_TABLE_RINGS, (str(dev), stream.cuda_stream), lambda: _TableRing(dev))
 
 
 def _upload_tables(tables, dev, stream, host_ok=False):
@@ -323,18 +334,11 @@ def _device_ctx(dev):
 
 
 def _arena(device) -> _PinnedIndexArena:
-    key = str(device)
-    if key not in _ARENAS:
-        _ARENAS[key] = _PinnedIndexArena(device)
-    return _ARENAS[key]
+    return _registered(_ARENAS, str(device), lambda: _PinnedIndexArena(device))
 
 
 def _ring(device, stream) -> _PinnedRing:
-    key = (str(device), stream.cuda_stream)
-    ring = _RINGS.get(key)
-    if ring is None:
-        ring = _RINGS[key] = _PinnedRing()
-    return ring
+    return _registered(_RINGS, (str(device), stream.cuda_stream), _PinnedRing)
 
 
 def to_device_i32(seqs, device):

@@ -188,3 +188,30 @@ def test_numpy_tile_tables_equal_the_reference_tiling():
                 a = _xcd_balanced(*ref)
                 b = _xcd_balanced(*got)
                 assert [list(x) for x in a] == [y.tolist() for y in b]
+
+
+def test_ring_registry_gives_every_thread_the_same_object():
+    """Two threads making their first call on one stream must share its
+    staging ring (a dropped ring's pinned block could be reused while a
+    kernel still reads group tables from it): creation runs under a lock and
+    re-checks the table."""
+    import threading
+    table, made = {}, []
+    gate = threading.Barrier(8)
+
+    def make():
+        made.append(object())
+        return made[-1]
+
+    got = []
+
+    def worker():
+        gate.wait()
+        got.append(nf4_grouped._registered(table, ("cuda:0", 1234), make))
+
+    ts = [threading.Thread(target=worker) for _ in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert len(made) == 1 and all(g is made[0] for g in got) and table[("cuda:0", 1234)] is made[0]

@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -51,6 +51,8 @@ SIGNATURES = {
                              _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_nf4_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                          _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
+    "gnf4_hip_nf4_fwd_fp32w": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                               _P, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_mxfp4_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                            _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_dgrad": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,

@@ -2062,17 +2062,49 @@ __device__ __forceinline__ void store_b_fwd(const BTileRegs<FMT>& r, const float
   }
 }
 
+// fp32-weight form (the reference's VARIANT 1, kernel/nf4_grouped.py:446-452,
+// which takes the fp32 products LUT x absmax into the dot): each fp32 weight
+// w = LUT * absmax (one rounding) splits into hi = bf16(w) and lo =
+// bf16(w - hi) (w - hi is exact in fp32), so hi + lo carries w to within
+// 2^-17 of its magnitude, and two MFMAs (hi, then lo) add both parts.
+template <int FMT>
+__device__ __forceinline__ void store_b_fwd_hilo(const BTileRegs<FMT>& r, const float2* tab,
+                                                 uint16_t* lds_hi, uint16_t* lds_lo) {
+  static_assert(FMT == kNF4, "MXFP4 weights are exact in bf16");
+  const int rr = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const unsigned lane_off = (unsigned)(threadIdx.x & 31) * 8u;
+  const int off = rr * kLdsRow + half * 32;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32x4_t vh, vl;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const unsigned addr = __builtin_amdgcn_perm(r.w[i], lane_off, 0x0C0C0000u | ((4u + b) << 8));
+      const float2 pr = *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(tab) + addr);
+      const float w0 = pr.x * r.s, w1 = pr.y * r.s;
+      const float h0 = bf16_round(w0), h1 = bf16_round(w1);
+      vh[b] = bf16x2_bits(h0, h1);
+      vl[b] = bf16x2_bits(w0 - h0, w1 - h1);
+    }
+    *reinterpret_cast<u32x4_t*>(lds_hi + off + 8 * i) = vh;
+    *reinterpret_cast<u32x4_t*>(lds_lo + off + 8 * i) = vl;
+  }
+}
+
 // Waves: WM x WN = 4. Wave tile (BM / WM) x (BN / WN) in 16 x 16 MFMA tiles.
 template <int BM> struct WaveGrid { static constexpr int WM = BM >= 64 ? 2 : 1; };
 
-template <int FMT, int BM>
+// HL: the fp32-weight form (store_b_fwd_hilo), NF4 only, BM <= 64 (LDS).
+template <int FMT, int BM, bool HL = false>
 __global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
+  static_assert(!HL || (FMT == kNF4 && BM <= 64), "fp32-weight tiles: NF4, at most 64 rows");
   constexpr int WM = WaveGrid<BM>::WM, WN = 4 / WM;
   constexpr int MT = BM / WM / 16, NT = kBN / WN / 16;
   constexpr int AP = (BM * 8 + kThreads - 1) / kThreads;
   __shared__ float2 s_tab[FMT == kNF4 ? kPairEntries : 1];
   __shared__ __attribute__((aligned(16))) uint16_t s_a[2][BM * kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_b[2][kBN * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t s_bl[HL ? 2 : 1][HL ? kBN * kLdsRow : 8];
   if constexpr (FMT == kNF4) init_pair_table(s_tab, nf4_lut_lane());
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2095,7 +2127,8 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
     load_a_tile<BM>(areg, p.a, p.lda, row0, rows, 0, p.K);
     load_b_fwd<FMT>(breg, p, e, n0, 0);
     store_a_tile<BM>(areg, s_a[0]);
-    store_b_fwd<FMT>(breg, s_tab, s_b[0]);
+    if constexpr (HL) store_b_fwd_hilo<FMT>(breg, s_tab, s_b[0], s_bl[0]);
+    else store_b_fwd<FMT>(breg, s_tab, s_b[0]);
     __syncthreads();
 
     f32x4_t acc[MT][NT];
@@ -2115,22 +2148,28 @@ __global__ void __launch_bounds__(kThreads, 1) k_gemm_fwd(const FwdArgs p) {
       const uint16_t* lb = s_b[cur];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        u32x4_t bop[NT];
+        u32x4_t bop[NT], bol[HL ? NT : 1];
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-          bop[j] = *reinterpret_cast<const u32x4_t*>(
-              lb + ((wn * NT + j) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
+        for (int j = 0; j < NT; ++j) {
+          const int bo = ((wn * NT + j) * 16 + l16) * kLdsRow + kk * 32 + q * 8;
+          bop[j] = *reinterpret_cast<const u32x4_t*>(lb + bo);
+          if constexpr (HL) bol[j] = *reinterpret_cast<const u32x4_t*>(&s_bl[cur][bo]);
+        }
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
           const u32x4_t aop = *reinterpret_cast<const u32x4_t*>(
               la + ((wm * MT + i) * 16 + l16) * kLdsRow + kk * 32 + q * 8);
 #pragma unroll
-          for (int j = 0; j < NT; ++j) acc[i][j] = mfma(aop, bop[j], acc[i][j]);
+          for (int j = 0; j < NT; ++j) {
+            acc[i][j] = mfma(aop, bop[j], acc[i][j]);
+            if constexpr (HL) acc[i][j] = mfma(aop, bol[j], acc[i][j]);
+          }
         }
       }
       if (more) {
         store_a_tile<BM>(areg, s_a[cur ^ 1]);
-        store_b_fwd<FMT>(breg, s_tab, s_b[cur ^ 1]);
+        if constexpr (HL) store_b_fwd_hilo<FMT>(breg, s_tab, s_b[cur ^ 1], s_bl[cur ^ 1]);
+        else store_b_fwd<FMT>(breg, s_tab, s_b[cur ^ 1]);
       }
       __syncthreads();
     }
@@ -4514,6 +4553,51 @@ int gnf4_hip_nf4_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* B,
   return gnf4_hip_grouped_fwd(GNF4_FMT_NF4, a, a_dtype, lda, B, stride_be, stride_bn, absmax,
                               stride_ae, stride_an, expert_ids, row_off, G, t_row0, t_rows,
                               t_group, n_mtiles, block_m, N, K, out, ldo, stream);
+}
+
+int gnf4_hip_nf4_fwd_fp32w(const void* a, int a_dtype, int64_t lda, const uint8_t* B,
+                           int64_t stride_be, int64_t stride_bn, const float* absmax,
+                           int64_t stride_ae, int64_t stride_an, const int32_t* expert_ids,
+                           const int32_t* t_row0, const int32_t* t_rows, const int32_t* t_group,
+                           int n_mtiles, int block_m, int64_t N, int64_t K, void* out,
+                           int64_t ldo, void* stream) {
+  if (a_dtype != GNF4_DTYPE_BF16 || N <= 0 || K <= 0 || K % 64 || n_mtiles < 0) return -1;
+  if (!a || !B || !absmax || !expert_ids || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  if (block_m != 16 && block_m != 32 && block_m != 64) return -1;
+  if (n_mtiles == 0) return 0;
+  if (!t_row0 || !t_rows || !t_group) return -1;
+  FwdArgs p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = absmax;
+  p.sse = stride_ae;
+  p.ssn = stride_an;
+  p.eids = expert_ids;
+  p.t_row0 = t_row0;
+  p.t_rows = t_rows;
+  p.t_group = t_group;
+  p.n_mtiles = n_mtiles;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  const int cus = device_cus();
+  if (cus <= 0) return -2;
+  const int64_t tiles = (int64_t)n_mtiles * ((N + kBN - 1) / kBN);
+  const unsigned grid = (unsigned)clamp_grid(tiles, cus);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (block_m) {
+    case 16: hipLaunchKernelGGL((k_gemm_fwd<kNF4, 16, true>), dim3(grid), dim3(kThreads), 0, s, p); break;
+    case 32: hipLaunchKernelGGL((k_gemm_fwd<kNF4, 32, true>), dim3(grid), dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL((k_gemm_fwd<kNF4, 64, true>), dim3(grid), dim3(kThreads), 0, s, p); break;
+  }
+  return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 int gnf4_hip_mxfp4_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* blocks,

@@ -66,7 +66,9 @@ def gemm_mxfp4_grouped(a_cat, blocks, scales, sizes, expert_ids,
     bf16 in the same group order. Groups of <= 16 rows take the decode kernel
     (each expert's weights streamed once); larger groups the tiled MFMA
     kernel (``block_m`` forces it). ``prefill_variant`` is accepted (0, 1, 3)
-    and does not change the result."""
+    and does not change the result: e2m1 x 2^(e - 127) is exact in bf16, so
+    every variant's weights (the reference's fp32 products of VARIANT 1
+    included) are the same values."""
     blocks = _flat_blocks(blocks)
     E, N, _ = blocks.shape
     T, K = a_cat.shape

@@ -717,8 +717,10 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
     return out
 
 
-def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
-    """Shared forward launcher for NF4 and MXFP4."""
+def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op, fp32w=False):
+    """Shared forward launcher for NF4 and MXFP4. ``fp32w`` (NF4): tiled
+    launches take the fp32-weight tiles (``gnf4_hip_nf4_fwd_fp32w``, the
+    reference's VARIANT 1), at most 64 rows per tile."""
     lib = _hiplib.load()
     E, N, half = W.shape
     T, K = a_cat.shape
@@ -751,6 +753,21 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op):
         e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
         # decode path: block_m carries the largest group size
         args = (e_ptr, r_ptr, G, None, None, None, 0, max_m)
+    elif fp32w:
+        bm = min(_kernel_block_m(block_m if block_m is not None else _prefill_block_m(max_m)), 64)
+        t0, tr, tg = _tiles_np(sizes_i, bm)
+        (e_p, t0_p, tr_p, tg_p), keep = _upload_tables((_np_ids(host_eids), t0, tr, tg), dev,
+                                                       stream)
+        e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
+        with _device_ctx(dev):
+            rc = lib.gnf4_hip_nf4_fwd_fp32w(
+                a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+                e_ptr, t0_p, tr_p, tg_p, len(t0), bm, N, K, out.data_ptr(), out.stride(0),
+                stream.cuda_stream)
+        del keep, eids_dev
+        _hiplib.check(rc, op)
+        return out
     else:
         bm = _fwd_block_m(max_m, N, K, block_m)
         t0, tr, tg = _tiles_np(sizes_i, bm)
@@ -854,10 +871,18 @@ def gemm_4bit_grouped(
 
     The reference's tuning knobs are accepted and validated so call sites keep
     working: ``decode_config`` (BLOCK_N, num_warps), ``split_k`` (>= 1),
-    ``prefill_config`` (BLOCK_N, num_warps, num_stages), ``prefill_variant``
-    (0, 1 or 3) and ``prefill_groups`` (1 or 2). They select Triton schedules
-    in the reference; here one HIP mainloop serves them all and they change
-    neither the path nor the result.
+    ``prefill_config`` (BLOCK_N, num_warps, num_stages) and
+    ``prefill_groups`` (1 or 2). They select Triton schedules in the
+    reference; here one HIP mainloop serves them all and they change neither
+    the path nor the result.
+
+    ``prefill_variant`` (0, 1 or 3) picks the tiled path's weight precision
+    as in the reference (kernel/nf4_grouped.py:438-452): ``None``, 0 and 3
+    run the default tiles, which round each decoded weight LUT x absmax to
+    bf16 once (the reference's VARIANT 3); 1 runs the fp32-weight tiles
+    (bf16 hi + lo parts of the fp32 weight, two MFMAs per slice: VARIANT 1's
+    fp32 weights) at about twice the matrix work. Decode-path calls (groups
+    of at most 16 rows, no ``block_m``) are fp32-accurate either way.
     """
     E, N, _ = B.shape
     T, K = a_cat.shape
@@ -895,7 +920,7 @@ def gemm_4bit_grouped(
         raise ValueError("a_cat, B and absmax must be on the same device")
     bm = block_m if (block_m is not None and max((int(m) for m in sizes), default=0) > 1) else None
     return _launch_fwd(_hiplib.FMT_NF4, a_cat, B, absmax, sizes, expert_ids, bm,
-                       "gemm_4bit_grouped")
+                       "gemm_4bit_grouped", fp32w=prefill_variant == 1)
 
 
 def dequant_ref(packed_row_major: torch.Tensor, absmax: torch.Tensor, N: int, K: int):

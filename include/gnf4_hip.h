@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 8
+#define GNF4_HIP_ABI_VERSION 9
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -119,6 +119,22 @@ int gnf4_hip_nf4_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *B,
                      const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
                      int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
                      void *stream);
+
+/* NF4 tiled forward with fp32-precision weights: the reference's default
+ * M-tile numerics (VARIANT 1, kernel/nf4_grouped.py:446-452: fp32 decoded
+ * weights LUT x absmax in the dot), selected there by prefill_variant=1.
+ * Each weight w = LUT[code] * absmax (fp32, one rounding) enters the bf16
+ * MFMA as hi = bf16(w) plus lo = bf16(w - hi), two MFMAs per k-slice, so the
+ * products carry w to within 2^-17 of |w| (the default tiled kernels round
+ * w to bf16 once). Tile table as for gnf4_hip_nf4_fwd's tiled path, with
+ * block_m in {16, 32, 64} (t_rows[i] <= block_m). Costs about twice the
+ * matrix work of the default tiles on a simpler kernel. 0 / -1 / -2. */
+int gnf4_hip_nf4_fwd_fp32w(const void *a, int a_dtype, int64_t lda, const uint8_t *B,
+                           int64_t stride_be, int64_t stride_bn, const float *absmax,
+                           int64_t stride_ae, int64_t stride_an, const int32_t *expert_ids,
+                           const int32_t *t_row0, const int32_t *t_rows,
+                           const int32_t *t_group, int n_mtiles, int block_m, int64_t N,
+                           int64_t K, void *out, int64_t ldo, void *stream);
 
 /* MXFP4 forward (e2m1 nibbles, e8m0 scale per 32). Replaces the launches of
  * gemm_mxfp4_grouped, reference kernel/mxfp4_grouped.py:146-171. */

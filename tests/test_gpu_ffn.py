@@ -337,3 +337,42 @@ def test_spin_expiry_poisons_the_rows_and_sets_the_error_word():
     assert nf4_ffn.ffn_sync_error() == timed_out     # sticky until cleared
     nf4_ffn.ffn_sync_clear()
     assert not nf4_ffn.ffn_sync_error()
+
+
+@pytest.mark.parametrize("B", [1, 4])
+def test_fused_hand_off_soak_in_graph_replays(B):
+    """Bounded soak of the fused launch's cross-workgroup hand-off (gate/up
+    units store h and then their flags with device-scope stores; down units
+    on any XCD poll the flags and then load h): 1500 replays of one captured
+    fused launch at Qwen3-30B-A3B shapes, the activations replaced before
+    each replay from a pool of 12, every replay compared bit for bit with
+    the three-launch composition of its activations; stops at the first
+    mismatch."""
+    nf4_ffn, nf4_grouped = _mods()
+    q = QWEN
+    gu_p, gu_a, dn_p, dn_a = _stack(q["E"], q["H"], q["K"], q["N_dn"], seed=140 + B)
+    g = torch.Generator().manual_seed(141 + B)
+    counts = torch.zeros(q["E"], dtype=torch.int64)
+    for _ in range(B):
+        counts[torch.randperm(q["E"], generator=g)[:8]] += 1
+    ids = torch.nonzero(counts).flatten().tolist()
+    sizes = counts[counts > 0].tolist()
+    T = sum(sizes)
+    pool = [rand_acts(T, q["K"], seed=150 + i) for i in range(12)]
+    want = [_composed(x, gu_p, gu_a, dn_p, dn_a, sizes, ids) for x in pool]
+    plan = nf4_grouped.GroupPlan(sizes, ids, "cuda")
+    x = pool[0].clone()
+    h = torch.empty(T, q["H"], dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(T, q["N_dn"], dtype=torch.bfloat16, device="cuda")
+    nf4_ffn.launch_ffn_planned(x, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)   # eager first
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        nf4_ffn.launch_ffn_planned(x, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)
+    for r in range(1500):
+        i = (r * 7) % len(pool)
+        x.copy_(pool[i])
+        graph.replay()
+        if not torch.equal(_bits(out), _bits(want[i])):
+            pytest.fail(f"replay {r} (activations {i}) differs from the composition")
+    assert not nf4_ffn.ffn_sync_error()

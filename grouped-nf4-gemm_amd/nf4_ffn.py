@@ -22,9 +22,11 @@ Two paths, both HIP:
 
 Numerics: gate and up are the bf16 outputs of the forward kernel, h is
 ``bf16(silu_locked(gate) * up)`` with the reference's locked fp32 silu
-(kernel/cpu_grouped.py:147-179), and the result is bf16. The fused launch
+(kernel/cpu_grouped.py:147-179), and the result is bf16. The fused call
 gives the same bits as the three-launch composition, which is how the tests
-pin it. Against the reference's fp32 CPU FFN the bound is the tolerance
+pin it. For one-row groups the fused call is two launches (the gate_up GEMV
+with the silu-multiply in its epilogue, then the down GEMV); larger groups
+run one launch whose down units wait on flags set by the gate/up units. Against the reference's fp32 CPU FFN the bound is the tolerance
 contract (docs/TOLERANCE_CONTRACT.md), like the forward op.
 """
 from __future__ import annotations
@@ -46,7 +48,9 @@ from nf4_grouped import (BLOCKSIZE, DECODE_MAX_ROWS, _aligned_rows, _bf16_activa
 # units per group): batch 1 (896 units) 13.7 us fused vs 15.3 us three-launch,
 # batch 2 23.1 vs 22.8, batch 4 48.5 vs 35.3 -- once the batched decode
 # kernels stream well, down units spinning in their slots cost more than the
-# saved launch. The fused launch wins up to about 1000 workgroup units.
+# saved launch. The fused launch wins up to about 1000 workgroup units. (At
+# batch 1 the fused call is now the two-launch GEMV form: 10.3 us per layer
+# against 12.6 us for three launches.)
 FUSED_MAX_UNITS = 1024
 
 
@@ -176,7 +180,7 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     ``a_cat [T, K]`` bf16 (fp16 / fp32 are rounded to bf16 first), rows sorted
     by group; ``sizes`` per-group row counts (zero-size groups allowed);
     ``expert_ids [G]`` list, CPU tensor or device tensor. Returns ``[T, N_dn]``
-    bf16. ``fused``: None picks the single fused launch when every group has at
+    bf16. ``fused``: None picks the fused call when every group has at
     most 16 rows and the launch has at most ``FUSED_MAX_UNITS`` workgroup
     units (where it measures faster); False forces the three-launch
     composition; True requires the fused launch. Both give the same bits."""

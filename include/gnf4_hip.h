@@ -156,8 +156,12 @@ int gnf4_hip_mxfp4_fwd(const void *a, int a_dtype, int64_t lda, const uint8_t *b
 int gnf4_hip_silu_mul(const void *gu, int64_t ldg, int64_t T, int64_t H, void *h,
                       int64_t ldh, void *stream);
 
-/* Fused NF4 expert FFN at decode, one launch: out = dn(silu(gate) * up) with
- * gate/up the two halves of a . W_gu^T. GPU counterpart of the reference's
+/* Fused NF4 expert FFN at decode, one call: out = dn(silu(gate) * up) with
+ * gate/up the two halves of a . W_gu^T. Groups of one row run two launches
+ * (the gate_up GEMV with the silu-multiply in its epilogue, then the down
+ * GEMV; `sync` unused); larger groups one launch whose down units wait for
+ * h through the sync flags. Same bits as gate_up forward -> silu-multiply ->
+ * down forward either way. GPU counterpart of the reference's
  * CPU gnf4_gemv_nf4_ffn_grouped (gnf4_native/cpu_kernels.c:948-986, spec
  * kernel/cpu_grouped.py:182-194), which has no GPU kernel there.
  *   a     [T, lda] bf16, rows sorted by group; every group <= 16 rows

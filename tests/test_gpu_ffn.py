@@ -341,10 +341,11 @@ def test_spin_expiry_poisons_the_rows_and_sets_the_error_word():
 
 @pytest.mark.parametrize("B", [1, 4])
 def test_fused_hand_off_soak_in_graph_replays(B):
-    """Bounded soak of the fused launch's cross-workgroup hand-off (gate/up
-    units store h and then their flags with device-scope stores; down units
-    on any XCD poll the flags and then load h): 1500 replays of one captured
-    fused launch at Qwen3-30B-A3B shapes, the activations replaced before
+    """Bounded soak of the fused call at Qwen3-30B-A3B shapes -- batch 4: the
+    single launch's cross-workgroup hand-off (gate/up units store h and then
+    their flags with device-scope stores; down units on any XCD poll the
+    flags and then load h); batch 1: its two-launch GEMV form -- 1500 replays
+    of one captured call, the activations replaced before
     each replay from a pool of 12, every replay compared bit for bit with
     the three-launch composition of its activations; stops at the first
     mismatch."""

@@ -733,7 +733,9 @@ def main():
                    "packed_bytes_per_step": model.packed_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(),
-                     "kernel": "k_decode_fwd<NF4> (gate_up, 8 experts x 1536 x 1024 B per launch)",
+                     "kernel": ("k_gemv_nf4<64, 1, 6, false, false> (gate_up, 8 experts x 1536 x "
+                                "1024 B per launch)" if args.batch == 1 else
+                                "NF4 decode launch of gate_up (kernel class by the largest group)"),
                      "avg_launch_us": round(avg_ms * 1e3, 3),
                      "timing": "HIP events around 20 replays of a graph of 48 back-to-back launches",
                      "floor": dict(floor_gu, note="same launch shape and bytes, nothing computed: "

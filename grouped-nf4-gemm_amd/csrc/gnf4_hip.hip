@@ -972,7 +972,13 @@ __device__ __forceinline__ void lds_barrier() {
 // (ldo) instead of the gate_up row: the bits of a plain launch followed by
 // k_silu_mul. RPW is even there; a wave covers RPW / 2 columns of h per row
 // group.
-template <int LR, int PPL, int RPW, bool GU = false>
+// ROWS: groups of up to four rows, one row per pass (a later pass reads the
+// same weight rows again, from L2, and decodes them again): each row's sums
+// follow the one-row order, so a row's bits do not depend on its group's
+// size. (Passes of two and four rows, with the activations held packed or
+// widened, were slower on MI355X: their registers halve the waves per SIMD,
+// and the lost latency hiding costs more than the repeated decode.)
+template <int LR, int PPL, int RPW, bool GU = false, bool ROWS = false>
 __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArgs p,
                                                                     const int ffn_h = 0) {
   static_assert(!GU || RPW % 2 == 0, "gate / up step pairs");
@@ -1015,98 +1021,111 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   auto step_ok = [&](int s) {
     return GU ? wrow0 + (s >> 1) * RS + rl < ffn_h : wrow0 + s * RS + rl < N32;
   };
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(q.a + (int64_t)r0 * q.lda, (int64_t)K32 * 2);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(q.B + e * q.sbe, q.N * q.sbn);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const char*>(q.S) + e * q.sse * 4,
-                                              q.N * q.ssn * 4);
-  // activations of the lane's pieces (64 bytes each), first in the queue
-  u32x4_t av[PPL][4];
-#pragma unroll
-  for (int i = 0; i < PPL; ++i) {
-    const int pc = j + i * LR;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) av[i][t] = buf_load16(ra, oob_unless(pc < PR, pc * 64 + t * 16));
-  }
-  u32x4_t wb[RPW][PPL];
-  unsigned sa[RPW][PPL];
-  auto issue = [&](int s) {
-    const int n = step_row(s);
-    const bool row_ok = step_ok(s);
+  // one pass over the workgroup's weight rows for group row rm (build: the
+  // first pass, which builds the table)
+  auto pass = [&](const int rm, const bool build) {
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(q.a + (int64_t)rm * q.lda, (int64_t)K32 * 2);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(q.B + e * q.sbe, q.N * q.sbn);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(static_cast<const char*>(q.S) + e * q.sse * 4,
+                                                q.N * q.ssn * 4);
+    // activations of the lane's pieces (64 bytes each), first in the queue
+    u32x4_t av[PPL][4];
 #pragma unroll
     for (int i = 0; i < PPL; ++i) {
       const int pc = j + i * LR;
-      const bool ok = row_ok && pc < PR;
-      wb[s][i] = buf_load16(rb, oob_unless(ok, n * (int)q.sbn + pc * 16));
-      sa[s][i] = __builtin_amdgcn_raw_buffer_load_b32(
-          rs, oob_unless(ok, (n * (int)q.ssn + (pc >> 1)) * 4), 0, 0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) av[i][t] = buf_load16(ra, oob_unless(pc < PR, pc * 64 + t * 16));
+    }
+    u32x4_t wb[RPW][PPL];
+    unsigned sa[RPW][PPL];
+    auto issue = [&](int s) {
+      const int n = step_row(s);
+      const bool row_ok = step_ok(s);
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) {
+        const int pc = j + i * LR;
+        const bool ok = row_ok && pc < PR;
+        wb[s][i] = buf_load16(rb, oob_unless(ok, n * (int)q.sbn + pc * 16));
+        sa[s][i] = __builtin_amdgcn_raw_buffer_load_b32(
+            rs, oob_unless(ok, (n * (int)q.ssn + (pc >> 1)) * 4), 0, 0);
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < D; ++s) issue(s);
+    __builtin_amdgcn_sched_barrier(0);
+    if (build) {   // uniform: the table once per workgroup
+      init_pair_table_imm(smem);
+      lds_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // widen the activations once
+    f32x4_t af[PPL][8];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const u32x4_t x = av[i][t];
+        af[i][2 * t] = f32x4_t{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xFFFF0000u),
+                               __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xFFFF0000u)};
+        af[i][2 * t + 1] = f32x4_t{__uint_as_float(x[2] << 16), __uint_as_float(x[2] & 0xFFFF0000u),
+                                   __uint_as_float(x[3] << 16), __uint_as_float(x[3] & 0xFFFF0000u)};
+      }
+    const unsigned lane_off = (unsigned)(uintptr_t)smem | (unsigned)(lane & 31) * 8u;
+    float v[RPW];
+#pragma unroll
+    for (int s = 0; s < RPW; ++s) {
+      if (s + D < RPW) issue(s + D);
+      __builtin_amdgcn_sched_barrier(0);
+      float slot = 0.0f;
+#pragma unroll
+      for (int i = 0; i < PPL; ++i) {
+        f32x2_t w[16];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            w[4 * jj + b] = lds_read8f(
+                __builtin_amdgcn_perm(wb[s][i][jj], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
+        float d[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const f32x4_t& x = af[i][2 * jj + (b >> 1)];
+            d[2 * (b & 1)] = __builtin_fmaf(w[4 * jj + b][0], x[2 * (b & 1)], d[2 * (b & 1)]);
+            d[2 * (b & 1) + 1] =
+                __builtin_fmaf(w[4 * jj + b][1], x[2 * (b & 1) + 1], d[2 * (b & 1) + 1]);
+          }
+        const float xv = ((d[0] + d[1]) + (d[2] + d[3])) * __uint_as_float(sa[s][i]);
+        const bool valid = j + i * LR < PR;
+        if (i == 0) slot = valid ? xv : 0.0f;
+        else slot = valid ? slot + xv : slot;
+      }
+      v[s] = group_sum<LR>(slot);
+    }
+    if constexpr (GU) {
+      float ov = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kCols; ++c) {
+        const float hv = silu_locked(bf16_round(v[2 * c])) * bf16_round(v[2 * c + 1]);
+        ov = j == c ? hv : ov;
+      }
+      const int n = wrow0 + j * RS + rl;
+      if (j < kCols && n < ffn_h) q.out[(int64_t)rm * q.ldo + n] = f32_to_bf16_bits(ov);
+    } else {
+      float ov = v[0];
+#pragma unroll
+      for (int s = 1; s < RPW; ++s) ov = j == s ? v[s] : ov;
+      const int n = wrow0 + j * RS + rl;
+      if (j < RPW && n < N32) q.out[(int64_t)rm * q.ldo + n] = f32_to_bf16_bits(ov);
     }
   };
-#pragma unroll
-  for (int s = 0; s < D; ++s) issue(s);
-  __builtin_amdgcn_sched_barrier(0);
-  init_pair_table_imm(smem);
-  lds_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  // widen the activations once
-  f32x4_t af[PPL][8];
-#pragma unroll
-  for (int i = 0; i < PPL; ++i)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const u32x4_t x = av[i][t];
-      af[i][2 * t] = f32x4_t{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xFFFF0000u),
-                             __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xFFFF0000u)};
-      af[i][2 * t + 1] = f32x4_t{__uint_as_float(x[2] << 16), __uint_as_float(x[2] & 0xFFFF0000u),
-                                 __uint_as_float(x[3] << 16), __uint_as_float(x[3] & 0xFFFF0000u)};
-    }
-  const unsigned lane_off = (unsigned)(uintptr_t)smem | (unsigned)(lane & 31) * 8u;
-  float v[RPW];
-#pragma unroll
-  for (int s = 0; s < RPW; ++s) {
-    if (s + D < RPW) issue(s + D);
-    __builtin_amdgcn_sched_barrier(0);
-    float slot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PPL; ++i) {
-      f32x2_t w[16];
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          w[4 * jj + b] = lds_read8f(
-              __builtin_amdgcn_perm(wb[s][i][jj], lane_off, 0x0C0C0000u | ((4u + b) << 8)));
-      float d[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const f32x4_t& x = af[i][2 * jj + (b >> 1)];
-          d[2 * (b & 1)] = __builtin_fmaf(w[4 * jj + b][0], x[2 * (b & 1)], d[2 * (b & 1)]);
-          d[2 * (b & 1) + 1] =
-              __builtin_fmaf(w[4 * jj + b][1], x[2 * (b & 1) + 1], d[2 * (b & 1) + 1]);
-        }
-      const float xv = ((d[0] + d[1]) + (d[2] + d[3])) * __uint_as_float(sa[s][i]);
-      const bool valid = j + i * LR < PR;
-      if (i == 0) slot = valid ? xv : 0.0f;
-      else slot = valid ? slot + xv : slot;
-    }
-    v[s] = group_sum<LR>(slot);
-  }
-  if constexpr (GU) {
-    float ov = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kCols; ++c) {
-      const float hv = silu_locked(bf16_round(v[2 * c])) * bf16_round(v[2 * c + 1]);
-      ov = j == c ? hv : ov;
-    }
-    const int n = wrow0 + j * RS + rl;
-    if (j < kCols && n < ffn_h) q.out[(int64_t)r0 * q.ldo + n] = f32_to_bf16_bits(ov);
+  if constexpr (!ROWS) {
+    pass(r0, true);
   } else {
-    float ov = v[0];
-#pragma unroll
-    for (int s = 1; s < RPW; ++s) ov = j == s ? v[s] : ov;
-    const int n = wrow0 + j * RS + rl;
-    if (j < RPW && n < N32) q.out[(int64_t)r0 * q.ldo + n] = f32_to_bf16_bits(ov);
+    // every row of the group in turn (one row without row offsets)
+    const int m_all = q.row_off ? ro_b - ro_a : 1;
+    for (int m = 0; m < m_all; ++m) pass(r0 + m, m == 0);
   }
 }
 
@@ -3665,26 +3684,27 @@ int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream)
 // GPT-OSS-20B gate_up 6 and down 3 per wave were the fastest of 1..12;
 // more, smaller workgroups and 1024-thread workgroups were slower). Returns
 // 1 when the launch is not for it.
-template <int FMT, int LR, int PPL, int RPW>
+template <int FMT, int LR, int PPL, int RPW, bool ROWS>
 int launch_gemv_inst(const FwdArgs& p, hipStream_t stream) {
   const int64_t rows_wg = 8 * RPW * (64 / LR);
   const int64_t gx = (p.N + rows_wg - 1) / rows_wg;
   if (gx > 0x7FFFFFFF) return -1;
   const dim3 grid((unsigned)gx, (unsigned)p.G, 1);
   if constexpr (FMT == kNF4)
-    hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW>), grid, dim3(512), 8 * kPairEntries, stream, p);
+    hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW, false, ROWS>), grid, dim3(512),
+                       8 * kPairEntries, stream, p, 0);
   else
     hipLaunchKernelGGL((k_gemv_mx<LR, PPL, RPW>), grid, dim3(512), 0, stream, p);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-template <int FMT, int LR, int PPL>
+template <int FMT, int LR, int PPL, bool ROWS = false>
 int launch_gemv_rpw(const FwdArgs& p, int rpw, hipStream_t stream) {
   switch (rpw) {
-    case 2: return launch_gemv_inst<FMT, LR, PPL, 2>(p, stream);
-    case 3: return launch_gemv_inst<FMT, LR, PPL, 3>(p, stream);
-    case 4: return launch_gemv_inst<FMT, LR, PPL, 4>(p, stream);
-    default: return launch_gemv_inst<FMT, LR, PPL, 6>(p, stream);
+    case 2: return launch_gemv_inst<FMT, LR, PPL, 2, ROWS>(p, stream);
+    case 3: return launch_gemv_inst<FMT, LR, PPL, 3, ROWS>(p, stream);
+    case 4: return launch_gemv_inst<FMT, LR, PPL, 4, ROWS>(p, stream);
+    default: return launch_gemv_inst<FMT, LR, PPL, 6, ROWS>(p, stream);
   }
 }
 
@@ -3697,6 +3717,27 @@ int gemv_slots(int64_t pr) {
   return 32 * ((pr + 31) / 32) < 64 * ((pr + 63) / 64) ? 32 : 64;
 }
 
+// The multi-row NF4 GEMV (k_gemv_nf4 with ROWS) takes decode launches whose
+// groups have at most four rows at 1024 < K <= 2048 (one 16-byte piece per
+// lane and row, 64 lanes a row), at most two rows at K <= 1024 (32 lanes a
+// row); larger groups, and larger K, keep the split-table kernels. The class
+// follows the largest group and K only, so a group's bits never depend on
+// the other groups of the launch. Measured on MI355X at Qwen3-30B-A3B shapes
+// (per launch, uniform top-8 of 128 experts): batch 2 gate_up 10.1 -> 8.9 us,
+// down (K = 768) 8.7 -> 7.2 us; batch 4 (largest group 3) gate_up 20.2 ->
+// 15.4 us. Where they lose: K = 768 at groups of 3..4 rows over many groups
+// (batch 16 layers whose largest group is 4: down 26.5 against 30.9 us), and
+// groups of 5..8 rows at K = 2048 (16 experts, 8 tokens: 14.3 against
+// 24.1 us).
+constexpr int kGemvMaxRows = 4;       // 1024 < K <= 2048
+constexpr int kGemvMaxRowsNarrow = 2; // K <= 1024
+
+// Whether an NF4 decode launch of groups of more than one row takes the GEMV.
+bool gemv_nf4_takes(const FwdArgs& p) {
+  if (p.max_m <= 1 || p.row_off == nullptr || p.K % 64 != 0 || p.K > 2048) return false;
+  return p.max_m <= (p.K > 1024 ? kGemvMaxRows : kGemvMaxRowsNarrow);
+}
+
 template <int FMT>
 int launch_gemv(const FwdArgs& p, hipStream_t stream) {
   if (p.K <= 0 || p.K % (FMT == kNF4 ? 64 : 32) != 0 || p.N <= 0 || p.G <= 0) return 1;
@@ -3707,12 +3748,20 @@ int launch_gemv(const FwdArgs& p, hipStream_t stream) {
   // 32-bit row offsets inside the expert's resources
   const int64_t sbytes = FMT == kNF4 ? 4 : 1;
   if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * sbytes > 0x7FFFFFFF) return 1;
+  if (p.max_m > 1 && (FMT != kNF4 || !gemv_nf4_takes(p))) return 1;
   const int cus = device_cus();
   if (cus <= 0) return -2;
   // row steps per wave: about one workgroup per CU over the launch's rows
   const int64_t per_step = (int64_t)cus * 8 * (64 / lr);
   const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
   const int rpw = want <= 2 ? 2 : want <= 3 ? 3 : want <= 4 ? 4 : 6;
+  if constexpr (FMT == kNF4) {
+    if (p.max_m > 1) {
+      if (ppl != 1) return 1;
+      if (lr == 32) return launch_gemv_rpw<FMT, 32, 1, true>(p, rpw, stream);
+      return launch_gemv_rpw<FMT, 64, 1, true>(p, rpw, stream);
+    }
+  }
   if (lr == 32) {
     if constexpr (FMT == kNF4) return launch_gemv_rpw<FMT, 32, 1>(p, rpw, stream);   // pr <= 32
     switch (ppl) {
@@ -3795,7 +3844,7 @@ int launch_decode_t(const FwdArgs& p, hipStream_t stream) {
   const int pa = decode_stage<FMT>(p.K, p.max_m, &a_bytes);
   const bool stage = pa > 0;
   const int sets = FMT != kNF4 ? 1 : p.max_m > 8 ? 2 : (p.max_m == 1 && pa > 0) ? 0 : 1;
-  if ((FMT == kNF4 && sets == 0) || (FMT == kMX && p.max_m == 1)) {
+  if ((FMT == kNF4 && (sets == 0 || gemv_nf4_takes(p))) || (FMT == kMX && p.max_m == 1)) {
     // one-row groups: the row-major GEMV (NF4: same bits as decode_unit's
     // one-row form)
     const int rc = launch_gemv<FMT>(p, stream);
@@ -4007,6 +4056,10 @@ int launch_stream(const FwdArgs& p, hipStream_t stream) {
 // several launches over consecutive group ranges.
 template <int FMT>
 int launch_decode(const FwdArgs& p, hipStream_t stream) {
+  if (FMT == kNF4 && gemv_nf4_takes(p) && p.G <= 65535) {
+    const int rc = launch_gemv<FMT>(p, stream);
+    if (rc <= 0) return rc;
+  }
   {
     const int rc = launch_rows<FMT>(p, stream);
     if (rc <= 0) return rc;
@@ -4093,36 +4146,46 @@ int launch_ffn_pa(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync
 
 // First stage of the one-row expert FFN (k_gemv_nf4 with the silu
 // epilogue): gu.out is h. Returns 1 when the shape is not for it.
-template <int LR, int PPL, int RPW>
+template <int LR, int PPL, int RPW, bool ROWS>
 int launch_gemv_gu_inst(const FwdArgs& p, int64_t H, hipStream_t stream) {
   const int64_t cols_wg = 8 * (RPW / 2) * (64 / LR);
   const int64_t gx = (H + cols_wg - 1) / cols_wg;
   if (gx > 0x7FFFFFFF) return -1;
-  hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW, true>), dim3((unsigned)gx, (unsigned)p.G, 1),
+  hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW, true, ROWS>), dim3((unsigned)gx, (unsigned)p.G, 1),
                      dim3(512), 8 * kPairEntries, stream, p, (int)H);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-template <int LR, int PPL>
+template <int LR, int PPL, bool ROWS = false>
 int launch_gemv_gu_rpw(const FwdArgs& p, int64_t H, int rpw, hipStream_t stream) {
   switch (rpw) {
-    case 2: return launch_gemv_gu_inst<LR, PPL, 2>(p, H, stream);
-    case 4: return launch_gemv_gu_inst<LR, PPL, 4>(p, H, stream);
-    default: return launch_gemv_gu_inst<LR, PPL, 6>(p, H, stream);
+    case 2: return launch_gemv_gu_inst<LR, PPL, 2, ROWS>(p, H, stream);
+    case 4: return launch_gemv_gu_inst<LR, PPL, 4, ROWS>(p, H, stream);
+    default: return launch_gemv_gu_inst<LR, PPL, 6, ROWS>(p, H, stream);
   }
 }
 
+// gate_up stage of the expert FFN in the GEMV class: one-row groups, or
+// groups the multi-row GEMV takes (gemv_nf4_takes). Returns 1 when the
+// launch is not for it.
 int launch_gemv_gu(const FwdArgs& p, int64_t H, hipStream_t stream) {
   const int64_t pr = p.K / 32;
   const int lr = pr <= 32 ? 32 : 64;
   const int64_t ppl = (pr + lr - 1) / lr;
   if (p.K % 64 || ppl > 4 || p.G > 65535) return 1;
   if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * 4 > 0x7FFFFFFF || H > 0x7FFFFFFF) return 1;
+  const bool multi = p.max_m > 1;
+  if (multi && !gemv_nf4_takes(p)) return 1;
   const int cus = device_cus();
   if (cus <= 0) return -2;
   const int64_t per_step = (int64_t)cus * 8 * (64 / lr);
   const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
   const int rpw = want <= 2 ? 2 : want <= 4 ? 4 : 6;
+  if (multi) {
+    if (ppl != 1) return 1;
+    if (lr == 32) return launch_gemv_gu_rpw<32, 1, true>(p, H, rpw, stream);
+    return launch_gemv_gu_rpw<64, 1, true>(p, H, rpw, stream);
+  }
   if (lr == 32) return launch_gemv_gu_rpw<32, 1>(p, H, rpw, stream);
   switch (ppl) {
     case 1: return launch_gemv_gu_rpw<64, 1>(p, H, rpw, stream);
@@ -4152,8 +4215,24 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& f
       return launch_decode<kNF4>(d1, stream);
     }
   }
+  bool gu_only = false;
+  if (gu.max_m > 1) {
+    // multi-row groups: the plain forward of each stage takes the GEMV class
+    // or the split-table kernels by its own K; the fused forms follow it
+    const bool g1 = gemv_nf4_takes(gu), g2 = gemv_nf4_takes(dn);
+    if (g1) {
+      const int r1 = launch_gemv_gu(gu, H, stream);
+      if (r1 <= 0) return r1 < 0 ? r1 : launch_decode<kNF4>(dn, stream);
+      return -1;
+    }
+    // the down stage alone takes the GEMV class: the single launch below
+    // runs its gate/up units only (h; with no down units they set no
+    // flags), and the down GEMV follows
+    if (g2) gu_only = true;
+  }
   constexpr int kW = 8;
-  const int64_t units = (int64_t)gu.G * (H / 16) + (int64_t)gu.G * ((dn.N + 31) / 32);
+  const int64_t units =
+      (int64_t)gu.G * (H / 16) + (gu_only ? 0 : (int64_t)gu.G * ((dn.N + 31) / 32));
   if (units <= 0) return 0;
   if (units > 0x7FFFFFFF) return -1;
   const int64_t kmax = gu.K > dn.K ? gu.K : dn.K;
@@ -4168,10 +4247,14 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& f
   const bool two1 = sets != 2 && ((gu.K + 127) / 128 + kW - 1) / kW > 1;
   const bool two2 = sets != 2 && ((dn.K + 127) / 128 + kW - 1) / kW > 1;
   const uint32_t n = (uint32_t)units;
-  if (two1 && two2) return launch_ffn_pa<2, 2>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
-  if (two1) return launch_ffn_pa<2, 1>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
-  if (two2) return launch_ffn_pa<1, 2>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
-  return launch_ffn_pa<1, 1>(gu, dn, H, fs, n, pa, sets, (int)lds, stream);
+  FwdArgs d = dn;
+  if (gu_only) d.N = 0;   // no down units: the gate/up units' flag rows are empty
+  const int rc = two1 && two2 ? launch_ffn_pa<2, 2>(gu, d, H, fs, n, pa, sets, (int)lds, stream)
+                 : two1       ? launch_ffn_pa<2, 1>(gu, d, H, fs, n, pa, sets, (int)lds, stream)
+                 : two2       ? launch_ffn_pa<1, 2>(gu, d, H, fs, n, pa, sets, (int)lds, stream)
+                              : launch_ffn_pa<1, 1>(gu, d, H, fs, n, pa, sets, (int)lds, stream);
+  if (rc || !gu_only) return rc;
+  return launch_decode<kNF4>(dn, stream);
 }
 
 // Workgroups per XCD range of the persistent k_prefill_w grid: one per CU

@@ -58,6 +58,33 @@ def _fused_units(G: int, H: int, n_dn: int) -> int:
     return G * (H // 16 + (n_dn + 31) // 32)
 
 
+#: Largest group of the multi-row decode GEMV (the library's kGemvMaxRows
+#: and kGemvMaxRowsNarrow): groups of up to 4 rows at 1024 < K <= 2048, up
+#: to 2 rows at K <= 1024, run as one-row passes of the GEMV.
+GEMV_MAX_ROWS = 4
+GEMV_MAX_ROWS_NARROW = 2
+
+
+def _gemv_stage(max_m: int, K: int) -> bool:
+    """Whether a decode launch of this largest group and K takes the GEMV
+    class (one-row groups always; multi-row ones as the library decides)."""
+    if max_m == 1:
+        return True
+    if K % 64 or K > 2048:
+        return False
+    return max_m <= (GEMV_MAX_ROWS if K > 1024 else GEMV_MAX_ROWS_NARROW)
+
+
+def _auto_fused(G: int, max_m: int, K: int, H: int, n_dn: int) -> bool:
+    """The fused call where it measures faster: always when its gate_up
+    stage is a GEMV (two launches, the silu-multiply in the first one's
+    epilogue), else while the single launch has at most FUSED_MAX_UNITS
+    units."""
+    if max_m > DECODE_MAX_ROWS:
+        return False
+    return _gemv_stage(max_m, K) or _fused_units(G, H, n_dn) <= FUSED_MAX_UNITS
+
+
 _SYNC_LOCK = threading.Lock()
 _SYNC = {}      # (device index, stream handle) -> current int32 sync words
 _RETIRED = []   # outgrown sync buffers: never freed (a captured graph may use them)
@@ -181,8 +208,11 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     by group; ``sizes`` per-group row counts (zero-size groups allowed);
     ``expert_ids [G]`` list, CPU tensor or device tensor. Returns ``[T, N_dn]``
     bf16. ``fused``: None picks the fused call when every group has at
-    most 16 rows and the launch has at most ``FUSED_MAX_UNITS`` workgroup
-    units (where it measures faster); False forces the three-launch
+    most 16 rows and either its gate_up stage is a GEMV (``_gemv_stage``:
+    groups of at most 4 rows at 1024 < K <= 2048, 2 at K <= 1024) or the
+    single launch has at most
+    ``FUSED_MAX_UNITS`` workgroup units (where it measures faster); False
+    forces the three-launch
     composition; True requires the fused launch. Both give the same bits."""
     _require_gpu(a_cat, "gemm_nf4_ffn_grouped",
                  "The CPU form is the reference's gemm_nf4_ffn_grouped_cpu; a "
@@ -195,7 +225,7 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
     G = len(sizes_i)
     max_m = max(sizes_i, default=0)
     if fused is None:
-        fused = max_m <= DECODE_MAX_ROWS and _fused_units(G, H, n_dn) <= FUSED_MAX_UNITS
+        fused = _auto_fused(G, max_m, K, H, n_dn)
     elif fused and max_m > DECODE_MAX_ROWS:
         raise ValueError(f"the fused FFN launch takes groups of at most {DECODE_MAX_ROWS} "
                          f"rows, got {max_m}")

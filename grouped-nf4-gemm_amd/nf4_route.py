@@ -263,7 +263,7 @@ def _expert_ffn_decode(a, plan, gu_packed, gu_absmax, dn_packed, dn_absmax, fuse
     H, n_dn = gu_packed.shape[1] // 2, dn_packed.shape[1]
     max_m = max(plan.max_rows_bound(), 1)
     if fused is None:
-        fused = nf4_ffn._fused_units(plan.slots, H, n_dn) <= nf4_ffn.FUSED_MAX_UNITS
+        fused = nf4_ffn._auto_fused(plan.slots, max_m, a.shape[1], H, n_dn)
     if fused:
         return nf4_ffn._launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, plan.eids,
                                      plan.row_off, plan.slots, max_m)
@@ -279,9 +279,12 @@ def moe_ffn(x, topk_ids, topk_weights, gu_packed, gu_absmax, dn_packed, dn_absma
     ``x [T, K]`` bf16; ``topk_ids [T, k]`` and ``topk_weights [T, k]`` on the
     device (from ``route_topk`` or the model's own router). With T <= 16
     (decode) nothing is read on the host: the routing tables stay on the
-    device and the expert FFN runs as the fused single launch (or, above
-    ``nf4_ffn.FUSED_MAX_UNITS`` workgroup units, as decode forward ->
-    silu-multiply -> decode forward), so the layer can be graph-captured.
+    device and the expert FFN runs as the fused call (two GEMV launches for
+    T <= 4 at 1024 < K <= 2048 and T <= 2 at K <= 1024, one launch
+    otherwise; above
+    ``nf4_ffn.FUSED_MAX_UNITS`` workgroup units of that launch, decode
+    forward -> silu-multiply -> decode forward), so the layer can be
+    graph-captured.
     Larger T reads the group sizes once and takes the tiled kernels."""
     _dev_check(x, "moe_ffn")
     T, K = x.shape

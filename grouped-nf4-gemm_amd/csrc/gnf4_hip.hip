@@ -3141,11 +3141,25 @@ __device__ __forceinline__ void prefill_w_tile(const FwdArgs& p, const PfTile t,
   }
 }
 
+// A tile table small enough to travel in the kernel arguments (n > 0): no
+// upload, so a call needs no copy ahead of its launch (and a captured graph
+// no copy node). grp holds the group index, or the expert id itself where
+// the caller knows the ids on the host (grp_is_expert). 3 KiB, inside the
+// kernel-argument limit with FwdArgs.
+constexpr int kPwMaxTiles = 256;
+struct PwTiles {
+  int32_t row0[kPwMaxTiles];
+  int32_t rows[kPwMaxTiles];
+  int32_t grp[kPwMaxTiles];
+  int32_t n;
+  int32_t grp_is_expert;
+};
+
 template <int FMT, bool DG = false>
 __global__ void __launch_bounds__(256, 1)
     k_prefill_w(const FwdArgs p, const int32_t* __restrict__ t_row0,
                 const int32_t* __restrict__ t_rows, const int32_t* __restrict__ t_group,
-                const int32_t* __restrict__ eids, uint16_t* __restrict__ out) {
+                const int32_t* __restrict__ eids, uint16_t* __restrict__ out, const PwTiles tt) {
   __shared__ __attribute__((aligned(16))) char smem[kPwLds];
   const int lut = FMT == kNF4 ? nf4_lut_lane() : 0;
   __builtin_amdgcn_sched_barrier(0);
@@ -3169,9 +3183,17 @@ __global__ void __launch_bounds__(256, 1)
     PfTile t;
     const int mt = (int)(tg / n_tiles);
     t.n0 = (int)(tg - (int64_t)mt * n_tiles) * kPfBN;
-    t.row0 = t_row0[mt];
-    t.rows = t_rows[mt];
-    t.e = eids[t_group[mt]];
+    if (tt.n > 0) {
+      // the table in the kernel arguments (scalar loads from the kernarg
+      // segment)
+      t.row0 = tt.row0[mt];
+      t.rows = tt.rows[mt];
+      t.e = tt.grp_is_expert ? tt.grp[mt] : eids[tt.grp[mt]];
+    } else {
+      t.row0 = t_row0[mt];
+      t.rows = t_rows[mt];
+      t.e = eids[t_group[mt]];
+    }
     // MFMAs for the tile's 32-row subtiles only
     switch ((t.rows + 31) >> 5) {
       case 8: prefill_w_tile<FMT, 8, DG>(p, t, smem, out, lut, first); break;
@@ -4257,6 +4279,12 @@ int launch_ffn(const FwdArgs& gu, const FwdArgs& dn, int64_t H, const FfnSync& f
   return launch_decode<kNF4>(dn, stream);
 }
 
+// An empty kernel-argument tile table: the kernel reads the device tables.
+const PwTiles& no_tiles() {
+  static const PwTiles empty{};
+  return empty;
+}
+
 // Workgroups per XCD range of the persistent k_prefill_w grid: one per CU
 // (each walks several tiles; the pair table is built once per workgroup), or
 // fewer when the XCD's range has fewer tiles.
@@ -4267,7 +4295,7 @@ int64_t prefill_w_per_xcd(int64_t tiles, int cus) {
 }
 
 template <int FMT>
-int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
+int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream, const PwTiles* tt = nullptr) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
   if (p.n_mtiles == 0) {
@@ -4277,6 +4305,7 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
     const bool pf_ok = p.N % 4 == 0 && p.ldo % 4 == 0 && p.K % kPfBK == 0 &&
                        (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPtBM &&
                        (int64_t)kPtBM * p.lda * 2 < 0x7FFFFFFF;
+    if (tt && block_m != kPtBM) return -1;   // kernel-argument tables: four-wave kernel only
     if (block_m == kPtBM) {
       // 256-row tiles: the host picks them only where the four-wave kernel
       // takes the shape
@@ -4286,7 +4315,7 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
       const int64_t per_x = prefill_w_per_xcd(tiles, cus);
       if (per_x * 8 > 0x7FFFFFFF) return -1;
       hipLaunchKernelGGL((k_prefill_w<FMT>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream, p,
-                         p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+                         p.t_row0, p.t_rows, p.t_group, p.eids, p.out, tt ? *tt : no_tiles());
       return hipGetLastError() == hipSuccess ? 0 : -2;
     }
     if (block_m > kPfBM) return -1;
@@ -4321,7 +4350,8 @@ int launch_fwd(const FwdArgs& p, int block_m, hipStream_t stream) {
 }
 
 template <int FMT>
-int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
+int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream,
+                 const PwTiles* tt = nullptr) {
   const int cus = device_cus();
   if (cus <= 0) return -2;
   {
@@ -4350,10 +4380,13 @@ int launch_dgrad(const DgradArgs& p, int block_m, hipStream_t stream) {
       const int64_t per_x = prefill_w_per_xcd(tiles, cus);
       if (per_x * 8 > 0x7FFFFFFF) return -1;
       hipLaunchKernelGGL((k_prefill_w<FMT, true>), dim3((unsigned)(per_x * 8)), dim3(256), 0, stream,
-                         f, p.t_row0, p.t_rows, p.t_group, p.eids, p.out);
+                         f, p.t_row0, p.t_rows, p.t_group, p.eids, p.out, tt ? *tt : no_tiles());
       return hipGetLastError() == hipSuccess ? 0 : -2;
     }
   }
+  // a kernel-argument tile table is for the four-wave kernel only: the others
+  // read device tables
+  if (tt) return -1;
   const bool tiled_ok = p.N % kDgStep == 0 && p.ldo % 4 == 0 &&
                         (reinterpret_cast<uintptr_t>(p.out) & 7) == 0 && block_m <= kPfBM &&
                         (int64_t)kPfBM * p.ldg * 2 < 0x7FFFFFFF && p.N * p.sbn < 0x7FFFFFFF;
@@ -4715,6 +4748,71 @@ int gnf4_hip_grouped_fwd(int fmt, const void* a, int a_dtype, int64_t lda, const
   return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, block_m, s) : launch_fwd<kMX>(p, block_m, s);
 }
 
+}  // extern "C"
+
+namespace {
+// Host tile tables -> the kernel-argument table; false when they do not fit
+// or are inconsistent (ids need a device table unless the tiles carry them).
+bool fill_tiles(PwTiles& tt, const int32_t* row0, const int32_t* rows, const int32_t* grp,
+                int group_is_expert, int n, const int32_t* expert_ids) {
+  if (n <= 0 || n > kPwMaxTiles || !row0 || !rows || !grp) return false;
+  if (!group_is_expert && !expert_ids) return false;
+  for (int i = 0; i < n; ++i) {
+    if (rows[i] <= 0 || rows[i] > kPtBM || row0[i] < 0 || grp[i] < 0) return false;
+    tt.row0[i] = row0[i];
+    tt.rows[i] = rows[i];
+    tt.grp[i] = grp[i];
+  }
+  tt.n = n;
+  tt.grp_is_expert = group_is_expert ? 1 : 0;
+  return true;
+}
+}  // namespace
+
+extern "C" {
+
+int gnf4_hip_grouped_fwd_tiles(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,
+                               int64_t stride_be, int64_t stride_bn, const void* scales,
+                               int64_t stride_se, int64_t stride_sn, const int32_t* expert_ids,
+                               const int32_t* tile_row0, const int32_t* tile_rows,
+                               const int32_t* tile_group, int tile_group_is_expert, int n_mtiles,
+                               int64_t N, int64_t K, void* out, int64_t ldo, void* stream) {
+  if (n_mtiles == 0) return 0;
+  if (n_mtiles < 0) return -1;
+  if (n_mtiles > kPwMaxTiles) return 1;   // the caller uploads the tables instead
+  PwTiles tt;
+  if (!fill_tiles(tt, tile_row0, tile_rows, tile_group, tile_group_is_expert, n_mtiles,
+                  expert_ids))
+    return -1;
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk) return -1;
+  if (!a || !B || !scales || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  FwdArgs p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.n_mtiles = n_mtiles;
+  p.G = 0;
+  p.max_m = kPtBM;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, kPtBM, s, &tt)
+                             : launch_fwd<kMX>(p, kPtBM, s, &tt);
+}
+
 int gnf4_hip_nf4_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t* B,
                      int64_t stride_be, int64_t stride_bn, const float* absmax,
                      int64_t stride_ae, int64_t stride_an, const int32_t* expert_ids,
@@ -4820,6 +4918,50 @@ int gnf4_hip_grouped_dgrad(int fmt, const void* grad_out, int g_dtype, int64_t l
   hipStream_t s = static_cast<hipStream_t>(stream);
   return fmt == GNF4_FMT_NF4 ? launch_dgrad<kNF4>(p, block_m, s)
                              : launch_dgrad<kMX>(p, block_m, s);
+}
+
+int gnf4_hip_grouped_dgrad_tiles(int fmt, const void* grad_out, int g_dtype, int64_t ldg,
+                                 const uint8_t* B, int64_t stride_be, int64_t stride_bn,
+                                 const void* scales, int64_t stride_se, int64_t stride_sn,
+                                 const int32_t* expert_ids, const int32_t* tile_row0,
+                                 const int32_t* tile_rows, const int32_t* tile_group,
+                                 int tile_group_is_expert, int n_mtiles, int64_t N, int64_t K,
+                                 void* out, int64_t ldo, void* stream) {
+  if (n_mtiles == 0) return 0;
+  if (n_mtiles < 0) return -1;
+  if (n_mtiles > kPwMaxTiles) return 1;   // the caller uploads the tables instead
+  PwTiles tt;
+  if (!fill_tiles(tt, tile_row0, tile_rows, tile_group, tile_group_is_expert, n_mtiles,
+                  expert_ids))
+    return -1;
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || g_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk) return -1;
+  if (!grad_out || !B || !scales || !out) return -1;
+  if (ldg < N || ldg % 8 || ldo < K || stride_bn % 4 || stride_be % 4 || !aligned16(grad_out) ||
+      (reinterpret_cast<uintptr_t>(B) & 3))
+    return -1;
+  DgradArgs p;
+  p.g = static_cast<const uint16_t*>(grad_out);
+  p.ldg = ldg;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.t_row0 = nullptr;
+  p.t_rows = nullptr;
+  p.t_group = nullptr;
+  p.n_mtiles = n_mtiles;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_dgrad<kNF4>(p, kPtBM, s, &tt)
+                             : launch_dgrad<kMX>(p, kPtBM, s, &tt);
 }
 
 int gnf4_hip_nf4_dgrad(const void* grad_out, int g_dtype, int64_t ldg, const uint8_t* B,

@@ -773,6 +773,19 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op, fp32w=Fal
         t0, tr, tg = _tiles_np(sizes_i, bm)
         if bm == 256:
             t0, tr, tg = _xcd_balanced(t0, tr, tg)
+            if len(t0) <= ARG_TILES_MAX:
+                a0, ar, ag, is_e, e_ptr = _arg_tiles(t0, tr, tg, eids_dev, expert_ids)
+                with _device_ctx(dev):
+                    rc = lib.gnf4_hip_grouped_fwd_tiles(
+                        fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                        W.data_ptr(), W.stride(0), W.stride(1),
+                        S.data_ptr(), S.stride(0), S.stride(1),
+                        e_ptr, a0.ctypes.data, ar.ctypes.data, ag.ctypes.data, is_e, len(a0),
+                        N, K, out.data_ptr(), out.stride(0), stream.cuda_stream)
+                if rc != 1:
+                    del eids_dev
+                    _hiplib.check(rc, op)
+                    return out
         (e_p, t0_p, tr_p, tg_p), keep = _upload_tables((_np_ids(host_eids), t0, tr, tg), dev,
                                                        stream)
         e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p
@@ -796,6 +809,23 @@ def _dgrad_block_m(max_rows: int, N: int, K: int) -> int:
     if max_rows > 128 and N % 64 == 0 and K % 64 == 0:
         return 256
     return _kernel_block_m(_prefill_block_m(max_rows))
+
+
+# Tile tables of at most this many m-tiles travel in the kernel arguments of
+# the 256-row kernels (gnf4_hip_grouped_fwd_tiles / _dgrad_tiles): no upload,
+# so no copy is enqueued ahead of the launch (in a captured graph: no copy
+# node and no dependency gap before the kernel).
+ARG_TILES_MAX = 256
+
+
+def _arg_tiles(t0, tr, tg, eids_dev, expert_ids):
+    """(row0, rows, group-or-expert, group_is_expert, expert-ids pointer) as
+    contiguous int32 host arrays for the kernel-argument table: with host
+    ids each tile carries its expert id, with device ids its group index."""
+    c = lambda x: np.ascontiguousarray(x, dtype=np.int32)
+    if eids_dev is not None:
+        return c(t0), c(tr), c(tg), 0, eids_dev.data_ptr()
+    return c(t0), c(tr), c(_np_ids(expert_ids)[tg]), 1, None
 
 
 def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
@@ -822,6 +852,18 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
     stream = torch.cuda.current_stream(dev)
+    if bm == 256 and len(t0) <= ARG_TILES_MAX:
+        a0, ar, ag, is_e, e_ptr = _arg_tiles(t0, tr, tg, eids_dev, expert_ids)
+        with _device_ctx(dev):
+            rc = lib.gnf4_hip_grouped_dgrad_tiles(
+                fmt, g.data_ptr(), _hiplib.DTYPE_BF16, g.stride(0),
+                W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+                e_ptr, a0.ctypes.data, ar.ctypes.data, ag.ctypes.data, is_e, len(a0),
+                N, K, out.data_ptr(), out.stride(0), stream.cuda_stream)
+        if rc != 1:
+            del eids_dev
+            _hiplib.check(rc, op)
+            return out
     (e_p, t0_p, tr_p, tg_p), keep = _upload_tables(
         (_np_ids([] if eids_dev is not None else expert_ids), t0, tr, tg), dev, stream)
     e_ptr = eids_dev.data_ptr() if eids_dev is not None else e_p

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 9
+#define GNF4_HIP_ABI_VERSION 10
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -109,6 +109,28 @@ int gnf4_hip_grouped_fwd(int fmt, const void *a, int a_dtype, int64_t lda,
                          const int32_t *t_row0, const int32_t *t_rows,
                          const int32_t *t_group, int n_mtiles, int block_m,
                          int64_t N, int64_t K, void *out, int64_t ldo, void *stream);
+
+/* Grouped forward on 256-row tiles with the tile table in host memory: the
+ * table (at most 256 m-tiles) travels in the kernel's arguments, so the call
+ * makes no copy ahead of its launch and a captured graph holds the kernel
+ * node alone. Same computation and bits as gnf4_hip_grouped_fwd with
+ * block_m = 256 and the same table. tile_row0 / tile_rows / tile_group are
+ * host arrays of n_mtiles int32, read before the call returns. With
+ * tile_group_is_expert = 1, tile_group holds each tile's expert id and
+ * expert_ids may be NULL; otherwise it holds group indices into the device
+ * array expert_ids. Returns 1, launching nothing, when n_mtiles > 256 (the
+ * caller uploads the table and calls gnf4_hip_grouped_fwd), -1 on a shape
+ * the 256-row kernel does not take or an inconsistent table. Replaces the
+ * same launch as gnf4_hip_grouped_fwd, reference
+ * kernel/nf4_grouped.py:750-906 (its tile tables go through
+ * to_device_i32, :229-331). */
+int gnf4_hip_grouped_fwd_tiles(int fmt, const void *a, int a_dtype, int64_t lda,
+                               const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                               const void *scales, int64_t stride_se, int64_t stride_sn,
+                               const int32_t *expert_ids, const int32_t *tile_row0,
+                               const int32_t *tile_rows, const int32_t *tile_group,
+                               int tile_group_is_expert, int n_mtiles, int64_t N, int64_t K,
+                               void *out, int64_t ldo, void *stream);
 
 /* NF4 forward (absmax fp32, block 64). Replaces the NF4 kernel launches of
  * gemm_4bit_grouped, reference kernel/nf4_grouped.py:750-906. */
@@ -254,6 +276,20 @@ int gnf4_hip_grouped_dgrad(int fmt, const void *grad_out, int g_dtype, int64_t l
                            const int32_t *t_rows, const int32_t *t_group, int n_mtiles,
                            int block_m, int64_t N, int64_t K, void *out, int64_t ldo,
                            void *stream);
+
+/* Grouped dgrad on 256-row tiles with the tile table in host memory, in the
+ * kernel's arguments (as gnf4_hip_grouped_fwd_tiles): same bits as
+ * gnf4_hip_grouped_dgrad with the same table. Needs N % 64 == 0 and
+ * K % 64 == 0 (-1 otherwise); returns 1 without launching when
+ * n_mtiles > 256. Replaces the launch of dgrad_4bit_grouped, reference
+ * kernel/nf4_grouped.py:1100-1120. */
+int gnf4_hip_grouped_dgrad_tiles(int fmt, const void *grad_out, int g_dtype, int64_t ldg,
+                                 const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                                 const void *scales, int64_t stride_se, int64_t stride_sn,
+                                 const int32_t *expert_ids, const int32_t *tile_row0,
+                                 const int32_t *tile_rows, const int32_t *tile_group,
+                                 int tile_group_is_expert, int n_mtiles, int64_t N, int64_t K,
+                                 void *out, int64_t ldo, void *stream);
 
 /* NF4 dgrad. Replaces the _dgrad_nf4_grouped launch of dgrad_4bit_grouped,
  * reference kernel/nf4_grouped.py:1100-1120. */

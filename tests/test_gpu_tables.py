@@ -64,3 +64,92 @@ def test_tables_larger_than_a_ring_part(fmt):
     first = op(a[:t0], W, S, sizes[:h], ids[:h])
     second = op(a[t0:], W, S, sizes[h:], ids[h:])
     assert torch.equal(whole.view(torch.int16), torch.cat([first, second]).view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("ids_on", ["host", "device"])
+def test_kernel_argument_tile_tables_give_the_same_bits(fmt, ids_on, monkeypatch):
+    """256-row tiled calls whose table fits the kernel arguments (no upload)
+    against the same calls with the table uploaded (ARG_TILES_MAX = 0):
+    bitwise, with host and device expert ids, ragged groups (empty, 1, 255,
+    256, 257, 700 rows)."""
+    op, stack = _ops()[fmt]
+    E, N, K = 64, 544, 1024
+    W, S = stack(E, N, K, seed=21)
+    sizes = [300, 0, 1, 255, 256, 257, 700, 40]
+    ids = [5, 9, 0, 63, 17, 2, 40, 33]
+    T = sum(sizes)
+    a = rand_acts(T, K, seed=22)
+    eids = torch.tensor(ids, dtype=torch.int32, device="cuda") if ids_on == "device" else ids
+    got = op(a, W, S, sizes, eids)
+    monkeypatch.setattr(nf4_grouped, "ARG_TILES_MAX", 0)
+    want = op(a, W, S, sizes, eids)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4"])
+@pytest.mark.parametrize("ids_on", ["host", "device"])
+def test_kernel_argument_tile_tables_dgrad(fmt, ids_on, monkeypatch):
+    """dgrad on 256-row tiles: kernel-argument table against the uploaded
+    one, bitwise."""
+    from mxfp4_grouped import dgrad_mxfp4_grouped
+    dg = nf4_grouped.dgrad_4bit_grouped if fmt == "nf4" else dgrad_mxfp4_grouped
+    _, stack = _ops()[fmt]
+    E, N, K = 32, 512, 768
+    W, S = stack(E, N, K, seed=23)
+    sizes = [129, 256, 0, 400, 3, 200]
+    ids = [31, 0, 7, 12, 30, 5]
+    go = (rand_acts(sum(sizes), N, seed=24).float() * 1e-2).to(torch.bfloat16)
+    eids = torch.tensor(ids, dtype=torch.int32, device="cuda") if ids_on == "device" else ids
+    got = dg(go, W, S, sizes, eids)
+    monkeypatch.setattr(nf4_grouped, "ARG_TILES_MAX", 0)
+    want = dg(go, W, S, sizes, eids)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_more_tiles_than_the_kernel_arguments_hold():
+    """300 groups of 200 rows: 300 m-tiles, more than the kernel-argument
+    table holds, so the call uploads the table; rows of a few groups against
+    single-group calls, bitwise."""
+    op, stack = _ops()["nf4"]
+    E, N, K = 8, 256, 1024
+    W, S = stack(E, N, K, seed=25)
+    G = 300
+    sizes = [200] * G
+    ids = [i % E for i in range(G)]
+    a = rand_acts(sum(sizes), K, seed=26)
+    assert G > nf4_grouped.ARG_TILES_MAX
+    got = op(a, W, S, sizes, ids)
+    for g in (0, 1, 150, 299):
+        r0 = 200 * g
+        one = op(a[r0:r0 + 200], W, S, [200], [ids[g]])
+        assert torch.equal(got[r0:r0 + 200].view(torch.int16), one.view(torch.int16)), g
+
+
+def test_kernel_argument_tables_in_graph_replays():
+    """A captured 256-row tiled call (kernel-argument table, so the graph has
+    no copy node) replayed with fresh activations: every replay equals the
+    eager call on the same activations."""
+    op, stack = _ops()["nf4"]
+    E, N, K = 16, 512, 1024
+    W, S = stack(E, N, K, seed=27)
+    sizes, ids = [300, 260, 0, 512], [3, 15, 8, 0]
+    a = rand_acts(sum(sizes), K, seed=28)
+    op(a, W, S, sizes, ids)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        op(a, W, S, sizes, ids)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            out = op(a, W, S, sizes, ids)
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(4):
+        a.copy_(rand_acts(sum(sizes), K, seed=40 + r))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = op(a, W, S, sizes, ids)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), r

@@ -262,7 +262,7 @@ class _TableRing:
                 ev = self.events[self.part]
                 if ev is None:
                     ev = self.events[self.part] = torch.cuda.Event()
-                ev.record(stream)
+                ev.record(stream.torch() if isinstance(stream, _CurStream) else stream)
                 self.part = (self.part + 1) % self.PARTS
                 self.off = 0
                 nxt = self.events[self.part]
@@ -636,8 +636,25 @@ def _check_host_ids(expert_ids, E: int) -> None:
         raise ValueError(f"expert id out of range [0, {E})")
 
 
+class _CurStream:
+    """The current stream of a device as a raw handle, read through torch's
+    C binding (``torch.cuda.current_stream`` builds a Python stream object per
+    call, several microseconds of a decode call's host time). ``torch()``
+    gives the stream object where one is needed (event records)."""
+
+    __slots__ = ("dev", "cuda_stream")
+
+    def __init__(self, dev):
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        self.dev = dev
+        self.cuda_stream = torch._C._cuda_getCurrentRawStream(idx)
+
+    def torch(self):
+        return torch.cuda.current_stream(self.dev)
+
+
 def _stream_ptr(dev) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    return _CurStream(dev).cuda_stream
 
 
 class GroupPlan:
@@ -738,7 +755,7 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op, fp32w=Fal
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
     host_eids = [] if eids_dev is not None else expert_ids
-    stream = torch.cuda.current_stream(dev)
+    stream = _CurStream(dev)
     if max_m <= DECODE_MAX_ROWS and block_m is None:
         if min(sizes_i) == 1 and max_m == 1:
             # one row per group: group g is row g, no offset table to upload
@@ -851,7 +868,7 @@ def _launch_dgrad(fmt: int, grad_out, W, S, sizes, expert_ids, op):
     eids_dev = _eids_device(expert_ids, dev)
     if eids_dev is None:
         _check_host_ids(expert_ids, E)
-    stream = torch.cuda.current_stream(dev)
+    stream = _CurStream(dev)
     if bm == 256 and len(t0) <= ARG_TILES_MAX:
         a0, ar, ag, is_e, e_ptr = _arg_tiles(t0, tr, tg, eids_dev, expert_ids)
         with _device_ctx(dev):

@@ -193,7 +193,8 @@ __global__ void __launch_bounds__(256) k_route_topk(const float* __restrict__ lo
 //
 // Outputs: eids[g], row_off[g] for g < slots (groups past the active count
 // are empty: row_off = N, eids = 0), row_off[slots] = N; order[r] = the row
-// placed at grouped position r; pos[i] = grouped position of row i (-1 for
+// placed at grouped position r (-1 for the positions past the valid rows,
+// as many as out-of-range ids); pos[i] = grouped position of row i (-1 for
 // an out-of-range expert id, which is also flagged in info[2]); info[0] =
 // active groups, info[1] = the largest group.
 // `order_lds`, when not null, receives a copy of `order` in LDS.
@@ -267,6 +268,12 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     eids[g] = 0;
     row_off[g] = (int32_t)N;
   }
+  // rows of out-of-range ids have no grouped position: the positions past
+  // the valid rows hold -1 (their gathered rows are zero)
+  for (int r = s_scan[kGroupThreads - 1] + tid; r < N; r += kGroupThreads) {
+    order[r] = -1;
+    if (order_lds) order_lds[r] = -1;
+  }
   __syncthreads();   // every wave's atomicMax on s_max has landed
   if (tid == 0) {
     row_off[slots] = (int32_t)N;
@@ -307,6 +314,111 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_groups(
   group_rows(ids, ids_stride, T, k, E, slots, eids, row_off, order, pos, info);
 }
 
+// group_rows' outputs computed by one wave (the calling wave, all 64 lanes)
+// for at most 64 rows (N = T * k <= 64: the decode prologue at a few
+// tokens), with no workgroup barrier. Counts by LDS atomics into s_cnt[E];
+// the exclusive scans over experts run across the lanes (lane l owns
+// experts [l P, l P + P), P = ceil(E / 64)) with shuffles; lane i places row
+// i after the earlier rows of its expert. Same outputs, bit for bit. `ids`
+// is the row-major [T, k] array (row i at ids[i]).
+__device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, int k, int E,
+                                                int slots, int32_t* __restrict__ eids,
+                                                int32_t* __restrict__ row_off,
+                                                int32_t* __restrict__ order,
+                                                int32_t* __restrict__ pos,
+                                                int32_t* __restrict__ info, int32_t* order_lds,
+                                                int32_t* s_cnt, int32_t* s_base) {
+  const int lane = threadIdx.x & 63;
+  const int N = (int)(T * k);
+  for (int e = lane; e < E; e += 64) s_cnt[e] = 0;
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the zeros before the counts
+  int bad = 0;
+  for (int i = lane; i < N; i += 64) {
+    const int64_t e = ids[i];
+    if (e >= 0 && e < E)
+      atomicAdd(&s_cnt[e], 1);
+    else
+      bad = 1;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+  // the lane's experts: totals and active counts, then exclusive scans
+  constexpr int kMaxP = kGroupMaxE / 64;
+  const int P = (E + 63) / 64;
+  int c[kMaxP];
+  int tot = 0, act = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxP; ++j) {
+    const int e = lane * P + j;
+    c[j] = j < P && e < E ? s_cnt[e] : 0;
+    tot += c[j];
+    act += c[j] > 0;
+    mx = c[j] > mx ? c[j] : mx;
+  }
+  int tot_x = tot, act_x = act;   // inclusive scans over lanes
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t1 = __shfl_up(tot_x, d, 64), a1 = __shfl_up(act_x, d, 64);
+    if (lane >= d) {
+      tot_x += t1;
+      act_x += a1;
+    }
+  }
+  int base = tot_x - tot, g = act_x - act;   // exclusive
+#pragma unroll
+  for (int j = 0; j < kMaxP; ++j) {
+    const int e = lane * P + j;
+    if (j < P && e < E) {
+      s_base[e] = base;
+      if (c[j] > 0) {
+        if (g < slots) {
+          eids[g] = e;
+          row_off[g] = base;
+        }
+        ++g;
+      }
+      base += c[j];
+    }
+  }
+  const int active = __shfl(act_x, 63, 64);
+  const int max_group = (int)wave_max_u32((uint32_t)mx);
+  // positions past the valid rows (out-of-range ids) hold -1
+  for (int r = __shfl(tot_x, 63, 64) + lane; r < N; r += 64) {
+    order[r] = -1;
+    if (order_lds) order_lds[r] = -1;
+  }
+  for (int gg = active + lane; gg < slots; gg += 64) {
+    eids[gg] = 0;
+    row_off[gg] = (int32_t)N;
+  }
+  if (lane == 0) {
+    row_off[slots] = (int32_t)N;
+    info[0] = active;
+    info[1] = max_group;
+    info[2] = bad;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // bases before the placement reads
+  // stable placement: row i goes after the earlier rows of its expert, whose
+  // number comes from a walk over the lanes' expert ids (no LDS round trip
+  // per expert)
+  const int i = lane;
+  const bool valid = i < N;
+  const int64_t e = valid ? ids[i] : -1;
+  const bool ok = valid && e >= 0 && e < E;
+  int rank = 0;
+  for (int j = 0; j < N; ++j) {
+    const int ej = __builtin_amdgcn_readlane((int)e, j);
+    rank += (j < i && ej == (int)e) ? 1 : 0;
+  }
+  if (valid && !ok) pos[i] = -1;
+  if (ok) {
+    const int p = s_base[e] + rank;
+    order[p] = (int32_t)i;
+    pos[i] = p;
+    if (order_lds) order_lds[p] = (int32_t)i;
+  }
+}
+
 // The whole decode routing prologue in one workgroup (T <= 16 tokens):
 // top-k of each token's logits by one wave (skipped when the caller passes
 // its own ids: logits == nullptr), the grouping, and the gather of the
@@ -325,6 +437,7 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     int64_t lda) {
   __shared__ int64_t s_ids[kDecodeMaxRows];
   __shared__ int32_t s_order[kDecodeMaxRows];
+  __shared__ int32_t s_cnt1[kGroupMaxE], s_base1[kGroupMaxE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = (int)(T * k);
   if (logits) {
@@ -342,7 +455,14 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     for (int i = threadIdx.x; i < N; i += kGroupThreads) s_ids[i] = idx[(i / k) * idx_stride + i % k];
   }
   __syncthreads();
-  group_rows(s_ids, k, T, k, E, slots, eids, row_off, order, pos, info, s_order);
+  // the grouping: by one wave, with no workgroup barriers, for up to 64 rows
+  if (N <= 64) {
+    if (wave == 0)
+      group_rows_wave(s_ids, T, k, E, slots, eids, row_off, order, pos, info, s_order, s_cnt1,
+                      s_base1);
+  } else {
+    group_rows(s_ids, k, T, k, E, slots, eids, row_off, order, pos, info, s_order);
+  }
   __syncthreads();
   // 32-bit index math (the host checks T * k * K < 2^31)
   const int vec = (int)(K / 8), total = N * vec;
@@ -354,7 +474,9 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
       const int q = q0 + u * kGroupThreads;
       if (q < total) {
         const int r = q / vec, c = (q - r * vec) * 8;
-        v[u] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)(s_order[r] / k) * ldx + c);
+        const int src = s_order[r];   // -1: no row (an out-of-range id)
+        v[u] = src >= 0 ? *reinterpret_cast<const u32x4_t*>(x + (int64_t)(src / k) * ldx + c)
+                        : u32x4_t{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
@@ -368,7 +490,8 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
   }
 }
 
-// out[r, :] = x[order[r] / k, :] for r < N. Eight bf16 per thread. Idx is
+// out[r, :] = x[order[r] / k, :] for r < N (zeros where order[r] < 0). Eight
+// bf16 per thread. Idx is
 // uint32_t whenever N * K / 8 < 2^32 (64-bit division is a long software
 // sequence on this GPU).
 template <class Idx>
@@ -380,9 +503,10 @@ __global__ void __launch_bounds__(256) k_gather_rows(const uint16_t* __restrict_
   for (Idx q = (Idx)blockIdx.x * blockDim.x + threadIdx.x; q < total;
        q += (Idx)gridDim.x * blockDim.x) {
     const Idx r = q / vec, c = (q - r * vec) * 8;
-    const int64_t src = order[r] / k;
+    const int32_t o = order[r];   // -1: no row (an out-of-range id), zeros
     *reinterpret_cast<u32x4_t*>(out + (int64_t)r * ldo + c) =
-        *reinterpret_cast<const u32x4_t*>(x + src * ldx + c);
+        o >= 0 ? *reinterpret_cast<const u32x4_t*>(x + (int64_t)(o / k) * ldx + c)
+               : u32x4_t{0u, 0u, 0u, 0u};
   }
 }
 

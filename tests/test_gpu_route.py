@@ -303,3 +303,28 @@ def test_bad_arguments_raise():
         r.route_topk(lg, 2, mode=3)
     with pytest.raises(ValueError):
         r.route_groups(torch.zeros(2, 2, dtype=torch.int64, device="cuda"), 600)
+
+
+@pytest.mark.parametrize("T,k,E", [(8, 8, 128), (9, 8, 128), (4, 16, 32), (2, 3, 512)])
+def test_one_launch_prologue_grouping_with_caller_ids(T, k, E):
+    """The one-launch prologue groups up to 64 rows with one wave and more
+    with the workgroup: with the caller's ids (repeated experts, and one id
+    out of range), every output equals the separate grouping kernel's.
+    (Regression: an out-of-range id left the last `order` entry unwritten,
+    and the gathers read it as a row index.)"""
+    r = _route()
+    g = torch.Generator().manual_seed(T * 100 + k)
+    ids = torch.randint(0, min(E, 6), (T, k), generator=g)   # few experts: many repeats
+    ids[T // 2, k - 1] = E + 3                                # out of range: flagged, dropped
+    ids = ids.to("cuda")
+    x = rand_acts(T, 256, seed=T + k)
+    plan, a, _, _ = r._route_decode(x, E, k, topk_ids=ids)
+    plan2 = r.route_groups(ids, E)
+    for f in ("eids", "row_off", "order", "pos", "info"):
+        assert torch.equal(getattr(plan, f), getattr(plan2, f)), f
+    assert plan.bad_ids()
+    # the one row of an out-of-range id has no grouped position: the last
+    # position holds -1 and gathers zeros, in both gathers
+    assert plan.order.cpu().tolist()[-1] == -1
+    assert torch.equal(_bits(a), _bits(r.gather_rows(x, plan2)))
+    assert torch.count_nonzero(a[-1].float()) == 0

@@ -112,6 +112,7 @@ class DecodeModel:
         self.gu, self.dn = weights[0][:L], weights[1][:L]
         rng = np.random.default_rng(seed + 7)
         self.routes = []
+        self.host_ids = []   # the same expert ids as host lists
         g = torch.Generator(device=dev).manual_seed(seed + 3)
         for _ in range(L):
             sizes, ids = route(rng, batch, cfg["top_k"], E)
@@ -120,6 +121,7 @@ class DecodeModel:
             h = torch.randn(T, cfg["dn"][1], generator=g, device=dev).to(torch.bfloat16)
             eids = torch.tensor(ids, dtype=torch.int32, device=dev)
             self.routes.append((sizes, eids, x, h))
+            self.host_ids.append(ids)
         N1, K1 = cfg["gu"]
         N2, K2 = cfg["dn"]
         self.bytes_gu = [len(r[0]) * N1 * K1 // 2 for r in self.routes]
@@ -134,13 +136,18 @@ class DecodeModel:
         from mxfp4_grouped import gemm_mxfp4_grouped
         return gemm_mxfp4_grouped
 
-    def step(self):
+    def step(self, device_ids=False):
+        """Every layer's gate_up and down op calls. The expert ids go in as
+        host lists (the group sizes are host lists in this API, so a
+        caller's ids are on the host with them), or as the device tensor
+        (device_ids: the kernels then read them from memory)."""
         op = self.op()
         outs = []
         for l in range(self.L):
             sizes, eids, x, h = self.routes[l]
-            outs.append(op(x, *self.gu[l], sizes, eids))
-            outs.append(op(h, *self.dn[l], sizes, eids))
+            ids = eids if device_ids else self.host_ids[l]
+            outs.append(op(x, *self.gu[l], sizes, ids))
+            outs.append(op(h, *self.dn[l], sizes, ids))
         return outs
 
     def plans(self):
@@ -661,6 +668,12 @@ def main():
     ms, graph = time_graph(model.step, args.steps, args.warmup, dev)
     value = model.packed_bytes / (ms * 1e-3) / 1e9
     log(f"[bench] step {ms:.4f} ms, {model.packed_bytes / 1e6:.1f} MB packed -> {value:.1f} GB/s")
+    del graph
+    ms_dev, graph_dev = time_graph(lambda: model.step(device_ids=True), args.steps, args.warmup, dev)
+    del graph_dev
+    step_dev = {"ms_per_step": round(ms_dev, 5),
+                "gbs": round(model.packed_bytes / (ms_dev * 1e-3) / 1e9, 2)}
+    log(f"[bench] step with device expert ids {ms_dev:.4f} ms -> {step_dev['gbs']} GB/s")
 
     avg_ms = model.kernel_ms("gu")
     per_launch = sum(model.bytes_gu) / len(model.bytes_gu)
@@ -673,7 +686,8 @@ def main():
     floor_gu, floor_dn = floor_report(model, "gu"), floor_report(model, "dn")
     log(f"[bench] floors: gate_up {json.dumps(floor_gu)}, down {json.dumps(floor_dn)}")
     extra = {"down_kernel": {"us": round(dn_ms * 1e3, 3), "gbs": round(dn_gbs, 1),
-                             "floor": floor_dn}}
+                             "floor": floor_dn},
+             "step_with_device_expert_ids": step_dev}
     extra[f"qwen3_nf4_ffn_b{args.batch}"] = ffn_report(model)
     log(f"[bench] ffn: {json.dumps(extra[f'qwen3_nf4_ffn_b{args.batch}'])}")
     extra["qwen3_nf4_decode_b1_eager_op_us"] = round(model.eager_us(), 2)
@@ -726,7 +740,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: N(0,0.02) weights NF4-quantized (one layer, cloned per layer), "
-                "N(0,1) bf16 activations, seeded uniform top-8 routing",
+                "N(0,1) bf16 activations, seeded uniform top-8 routing; expert ids passed as host "
+                "lists with the host group sizes (the device-tensor form: "
+                "extra.step_with_device_expert_ids)",
         "config": {"workload": "qwen3-30b-a3b nf4 decode: 48 layers x (gate_up 1536x2048 + down 2048x768), "
                                f"E=128, top-8, batch {args.batch}, HIP graph replay",
                    "batch": args.batch, "layers": model.L,

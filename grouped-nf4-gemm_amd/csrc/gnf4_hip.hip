@@ -325,6 +325,22 @@ struct FwdArgs {
   int64_t N, K;
   uint16_t* out;            // [T, ldo] bf16
   int64_t ldo;
+  // host only: group ids and row offsets to pass in the GEMV kernels'
+  // arguments (GemvIds), or null (the kernels read eids / row_off)
+  const struct GemvIds* ids_inline;
+};
+
+// The expert ids (and row offsets) of a decode launch of at most
+// kGemvIdsMax groups, in the GEMV kernels' arguments (n > 0): the kernel
+// reads them from the kernarg segment it loads anyway, instead of a table
+// in memory behind it (one dependent round trip before the first weight
+// load). ro holds G + 1 offsets when has_ro, else group g is row g.
+constexpr int kGemvIdsMax = 384;
+struct GemvIds {
+  int32_t e[kGemvIdsMax];
+  int32_t ro[kGemvIdsMax + 1];
+  int32_t n;
+  int32_t has_ro;
 };
 
 constexpr int kOOB = (int)0x80000000;  // buffer offset past every resource: loads 0
@@ -980,33 +996,48 @@ __device__ __forceinline__ void lds_barrier() {
 // and the lost latency hiding costs more than the repeated decode.)
 template <int LR, int PPL, int RPW, bool GU = false, bool ROWS = false>
 __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArgs p,
-                                                                    const int ffn_h = 0) {
+                                                                    const int ffn_h,
+                                                                    const GemvIds gi) {
   static_assert(!GU || RPW % 2 == 0, "gate / up step pairs");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int RS = 64 / LR;          // rows per wave step
   constexpr int D = RPW < 2 ? RPW : 2; // row steps in flight
   const FwdArgs q = p;
+  // kernel-argument ids: loaded with the other arguments, in one round trip
+  // (a clamped index keeps every load inside the arguments)
+  const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
+  const int gi_n = gi.n, gi_ro = gi.has_ro, gi_e = gi.e[gc], gi_r0 = gi.ro[gc],
+            gi_r1 = gi.ro[gc + 1];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
                "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
-               "s"(q.ldo));
+               "s"(q.ldo), "s"(gi_n), "s"(gi_ro), "s"(gi_e), "s"(gi_r0), "s"(gi_r1));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
   const int g = (int)blockIdx.y;
   // the expert id and the group's row in one round trip of scalar loads
-  const int32_t* ce = q.eids + g;
-  const int32_t* cr = q.row_off ? q.row_off + g : ce;
-  const int32_t* cr1 = q.row_off ? cr + 1 : ce;
   int e32, ro_a, ro_b;
-  asm volatile(
-      "s_load_dword %0, %3, 0x0\n\t"
-      "s_load_dword %1, %4, 0x0\n\t"
-      "s_load_dword %2, %5, 0x0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
-      : "s"(ce), "s"(cr), "s"(cr1)
-      : "memory");
-  const int r0 = q.row_off ? ro_a : g;
-  if (q.row_off && ro_b - ro_a <= 0) return;   // empty group (uniform)
+  bool has_ro;
+  if (gi_n > 0) {   // ids in the kernel arguments
+    has_ro = gi_ro != 0;
+    e32 = gi_e;
+    ro_a = has_ro ? gi_r0 : 0;
+    ro_b = has_ro ? gi_r1 : 1;
+  } else {
+    has_ro = q.row_off != nullptr;
+    const int32_t* ce = q.eids + g;
+    const int32_t* cr = has_ro ? q.row_off + g : ce;
+    const int32_t* cr1 = has_ro ? cr + 1 : ce;
+    asm volatile(
+        "s_load_dword %0, %3, 0x0\n\t"
+        "s_load_dword %1, %4, 0x0\n\t"
+        "s_load_dword %2, %5, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+        : "s"(ce), "s"(cr), "s"(cr1)
+        : "memory");
+  }
+  const int r0 = has_ro ? ro_a : g;
+  if (has_ro && ro_b - ro_a <= 0) return;   // empty group (uniform)
   const int64_t e = e32;
   const int K32 = (int)q.K;
   const int PR = K32 >> 5;
@@ -1124,7 +1155,7 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
     pass(r0, true);
   } else {
     // every row of the group in turn (one row without row offsets)
-    const int m_all = q.row_off ? ro_b - ro_a : 1;
+    const int m_all = has_ro ? ro_b - ro_a : 1;
     for (int m = 0; m < m_all; ++m) pass(r0 + m, m == 0);
   }
 }
@@ -1143,30 +1174,44 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
 // chunk by element shuffles: hipcc 7.2 folds a bit_cast of dword 1..3 of a
 // u32x4 into a bf16x2 to dword 0.)
 template <int LR, int PPL, int RPW>
-__global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p) {
+__global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p, const GemvIds gi) {
   constexpr int RS = 64 / LR;
   constexpr int D = RPW < 2 ? RPW : 2;
   const FwdArgs q = p;
+  // kernel-argument ids: loaded with the other arguments, in one round trip
+  // (a clamped index keeps every load inside the arguments)
+  const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
+  const int gi_n = gi.n, gi_ro = gi.has_ro, gi_e = gi.e[gc], gi_r0 = gi.ro[gc],
+            gi_r1 = gi.ro[gc + 1];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
                "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
-               "s"(q.ldo));
+               "s"(q.ldo), "s"(gi_n), "s"(gi_ro), "s"(gi_e), "s"(gi_r0), "s"(gi_r1));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
   const int g = (int)blockIdx.y;
-  const int32_t* ce = q.eids + g;
-  const int32_t* cr = q.row_off ? q.row_off + g : ce;
-  const int32_t* cr1 = q.row_off ? cr + 1 : ce;
   int e32, ro_a, ro_b;
-  asm volatile(
-      "s_load_dword %0, %3, 0x0\n\t"
-      "s_load_dword %1, %4, 0x0\n\t"
-      "s_load_dword %2, %5, 0x0\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
-      : "s"(ce), "s"(cr), "s"(cr1)
-      : "memory");
-  const int r0 = q.row_off ? ro_a : g;
-  if (q.row_off && ro_b - ro_a <= 0) return;   // empty group (uniform)
+  bool has_ro;
+  if (gi_n > 0) {   // ids in the kernel arguments
+    has_ro = gi_ro != 0;
+    e32 = gi_e;
+    ro_a = has_ro ? gi_r0 : 0;
+    ro_b = has_ro ? gi_r1 : 1;
+  } else {
+    has_ro = q.row_off != nullptr;
+    const int32_t* ce = q.eids + g;
+    const int32_t* cr = has_ro ? q.row_off + g : ce;
+    const int32_t* cr1 = has_ro ? cr + 1 : ce;
+    asm volatile(
+        "s_load_dword %0, %3, 0x0\n\t"
+        "s_load_dword %1, %4, 0x0\n\t"
+        "s_load_dword %2, %5, 0x0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
+        : "s"(ce), "s"(cr), "s"(cr1)
+        : "memory");
+  }
+  const int r0 = has_ro ? ro_a : g;
+  if (has_ro && ro_b - ro_a <= 0) return;   // empty group (uniform)
   const int64_t e = e32;
   const int K32 = (int)q.K;
   const int PR = K32 >> 5;
@@ -3699,6 +3744,12 @@ int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream)
   return 0;
 }
 
+// The kernel-argument ids of a launch (empty: the kernels read the tables).
+const GemvIds& gemv_ids_of(const FwdArgs& p) {
+  static const GemvIds empty{};
+  return p.ids_inline ? *p.ids_inline : empty;
+}
+
 // One-row decode launch (k_gemv_nf4, k_gemv_mx): every group exactly one
 // row and at most four pieces per lane (NF4 K <= 8192). Row steps per wave:
 // enough for about one workgroup per CU over the launch's rows, at most six
@@ -3706,6 +3757,7 @@ int launch_decode_inst(const FwdArgs& p, dim3 grid, int lds, hipStream_t stream)
 // GPT-OSS-20B gate_up 6 and down 3 per wave were the fastest of 1..12;
 // more, smaller workgroups and 1024-thread workgroups were slower). Returns
 // 1 when the launch is not for it.
+
 template <int FMT, int LR, int PPL, int RPW, bool ROWS>
 int launch_gemv_inst(const FwdArgs& p, hipStream_t stream) {
   const int64_t rows_wg = 8 * RPW * (64 / LR);
@@ -3714,9 +3766,9 @@ int launch_gemv_inst(const FwdArgs& p, hipStream_t stream) {
   const dim3 grid((unsigned)gx, (unsigned)p.G, 1);
   if constexpr (FMT == kNF4)
     hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW, false, ROWS>), grid, dim3(512),
-                       8 * kPairEntries, stream, p, 0);
+                       8 * kPairEntries, stream, p, 0, gemv_ids_of(p));
   else
-    hipLaunchKernelGGL((k_gemv_mx<LR, PPL, RPW>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((k_gemv_mx<LR, PPL, RPW>), grid, dim3(512), 0, stream, p, gemv_ids_of(p));
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -3755,9 +3807,13 @@ constexpr int kGemvMaxRows = 4;       // 1024 < K <= 2048
 constexpr int kGemvMaxRowsNarrow = 2; // K <= 1024
 
 // Whether an NF4 decode launch of groups of more than one row takes the GEMV.
+bool gemv_nf4_takes_rows(int max_m, int64_t K) {
+  if (max_m <= 1 || K % 64 != 0 || K > 2048) return false;
+  return max_m <= (K > 1024 ? kGemvMaxRows : kGemvMaxRowsNarrow);
+}
 bool gemv_nf4_takes(const FwdArgs& p) {
-  if (p.max_m <= 1 || p.row_off == nullptr || p.K % 64 != 0 || p.K > 2048) return false;
-  return p.max_m <= (p.K > 1024 ? kGemvMaxRows : kGemvMaxRowsNarrow);
+  const bool has_ro = p.ids_inline ? p.ids_inline->has_ro != 0 : p.row_off != nullptr;
+  return has_ro && gemv_nf4_takes_rows(p.max_m, p.K);
 }
 
 template <int FMT>
@@ -4174,7 +4230,7 @@ int launch_gemv_gu_inst(const FwdArgs& p, int64_t H, hipStream_t stream) {
   const int64_t gx = (H + cols_wg - 1) / cols_wg;
   if (gx > 0x7FFFFFFF) return -1;
   hipLaunchKernelGGL((k_gemv_nf4<LR, PPL, RPW, true, ROWS>), dim3((unsigned)gx, (unsigned)p.G, 1),
-                     dim3(512), 8 * kPairEntries, stream, p, (int)H);
+                     dim3(512), 8 * kPairEntries, stream, p, (int)H, gemv_ids_of(p));
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -4770,6 +4826,63 @@ bool fill_tiles(PwTiles& tt, const int32_t* row0, const int32_t* rows, const int
 }  // namespace
 
 extern "C" {
+
+int gnf4_hip_grouped_decode_ids(int fmt, const void* a, int a_dtype, int64_t lda,
+                                const uint8_t* B, int64_t stride_be, int64_t stride_bn,
+                                const void* scales, int64_t stride_se, int64_t stride_sn,
+                                const int32_t* expert_ids, const int32_t* row_off, int G,
+                                int max_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                                void* stream) {
+  if (G == 0) return 0;
+  if (G < 0 || !expert_ids) return -1;
+  if (G > kGemvIdsMax || max_m < 1 || max_m > 16) return 1;   // the caller uploads the tables
+  if (max_m > 1 && !row_off) return -1;
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk) return -1;
+  if (!a || !B || !scales || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  GemvIds gi;
+  for (int g = 0; g < G; ++g) {
+    if (expert_ids[g] < 0) return -1;
+    gi.e[g] = expert_ids[g];
+  }
+  gi.has_ro = row_off ? 1 : 0;
+  if (row_off)
+    for (int g = 0; g <= G; ++g) {
+      if (row_off[g] < 0 || (g > 0 && row_off[g] < row_off[g - 1])) return -1;
+      gi.ro[g] = row_off[g];
+    }
+  gi.n = G;
+  FwdArgs p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.G = G;
+  p.max_m = max_m;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  p.ids_inline = &gi;
+  // the tables' pointers stay null: only the GEMV kernels run here, and they
+  // read the kernel-argument ids; a launch no GEMV class takes returns 1
+  // before anything is launched
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fmt == GNF4_FMT_NF4) {
+    if (max_m > 1 && !gemv_nf4_takes_rows(max_m, K)) return 1;
+    return launch_gemv<kNF4>(p, s);
+  }
+  if (max_m > 1) return 1;
+  return launch_gemv<kMX>(p, s);
+}
 
 int gnf4_hip_grouped_fwd_tiles(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,
                                int64_t stride_be, int64_t stride_bn, const void* scales,

@@ -681,12 +681,16 @@ class GroupPlan:
         self.user_block_m = block_m
         self.decode = self.max_m <= DECODE_MAX_ROWS and block_m is None
         self.eids = torch.tensor(ids, dtype=torch.int32, device=self.device)
+        self.host_ids = np.asarray([int(e) for e in ids], dtype=np.int32)
+        self.host_row_off = None
         self._tables = {}
         if self.decode:
             row_off = [0]
             for m in sizes_i:
                 row_off.append(row_off[-1] + m)
             self.row_off = torch.tensor(row_off, dtype=torch.int32, device=self.device)
+            if not self.one_row_each:
+                self.host_row_off = np.asarray(row_off, dtype=np.int32)
         else:
             self.row_off = None
             if shape is not None:
@@ -725,6 +729,17 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
                    _scales_view(S))
     if out is None:
         out = torch.empty(T, N, dtype=torch.bfloat16, device=dev)
+    if plan.decode and 0 < plan.G <= IDS_ARG_MAX:
+        ro = plan.host_row_off
+        with torch.cuda.device(dev):
+            rc = lib.gnf4_hip_grouped_decode_ids(
+                fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+                plan.host_ids.ctypes.data, ro.ctypes.data if ro is not None else None, plan.G,
+                plan.max_m, N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+        if rc != 1:
+            _hiplib.check(rc, "launch_planned")
+            return out
     with torch.cuda.device(dev):
         rc = lib.gnf4_hip_grouped_fwd(
             fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
@@ -756,6 +771,23 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op, fp32w=Fal
         _check_host_ids(expert_ids, E)
     host_eids = [] if eids_dev is not None else expert_ids
     stream = _CurStream(dev)
+    if max_m <= DECODE_MAX_ROWS and block_m is None and eids_dev is None and G <= IDS_ARG_MAX:
+        # host ids: in the kernel's arguments where a GEMV class takes the
+        # launch (no table read ahead of the weights, no upload)
+        ids32 = _np_ids(expert_ids)
+        ro = None
+        if not (min(sizes_i) == 1 and max_m == 1):
+            ro = np.zeros(G + 1, dtype=np.int32)
+            np.cumsum(np.asarray(sizes_i, dtype=np.int32), out=ro[1:])
+        with _device_ctx(dev):
+            rc = lib.gnf4_hip_grouped_decode_ids(
+                fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+                ids32.ctypes.data, ro.ctypes.data if ro is not None else None, G, max_m,
+                N, K, out.data_ptr(), out.stride(0), stream.cuda_stream)
+        if rc != 1:
+            _hiplib.check(rc, op)
+            return out
     if max_m <= DECODE_MAX_ROWS and block_m is None:
         if min(sizes_i) == 1 and max_m == 1:
             # one row per group: group g is row g, no offset table to upload
@@ -827,6 +859,11 @@ def _dgrad_block_m(max_rows: int, N: int, K: int) -> int:
         return 256
     return _kernel_block_m(_prefill_block_m(max_rows))
 
+
+# Decode launches of at most this many groups with host-known expert ids pass
+# the ids (and row offsets) in the GEMV kernels' arguments
+# (gnf4_hip_grouped_decode_ids).
+IDS_ARG_MAX = 384
 
 # Tile tables of at most this many m-tiles travel in the kernel arguments of
 # the 256-row kernels (gnf4_hip_grouped_fwd_tiles / _dgrad_tiles): no upload,

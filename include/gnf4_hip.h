@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 10
+#define GNF4_HIP_ABI_VERSION 11
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -109,6 +109,27 @@ int gnf4_hip_grouped_fwd(int fmt, const void *a, int a_dtype, int64_t lda,
                          const int32_t *t_row0, const int32_t *t_rows,
                          const int32_t *t_group, int n_mtiles, int block_m,
                          int64_t N, int64_t K, void *out, int64_t ldo, void *stream);
+
+/* Grouped decode forward with the expert ids (and row offsets) in host
+ * memory, for launches of at most 384 groups in a GEMV class: groups of one
+ * row (NF4 and MXFP4), or NF4 groups of up to 4 rows at 1024 < K <= 2048 (2
+ * rows at K <= 1024). The ids travel in the kernel's arguments, so the
+ * kernel reads no table before its first weight load, the call makes no
+ * upload, and a captured call is the kernel node alone. Same bits as
+ * gnf4_hip_grouped_fwd's decode path with the same ids. expert_ids[G] and
+ * row_off[G + 1] (NULL: group g is row g, max_m = 1) are read before the
+ * call returns. Returns 1, launching nothing, when G > 384 or no GEMV class
+ * takes the launch (the caller then uploads the tables and calls
+ * gnf4_hip_grouped_fwd). Replaces the decode launches of gemm_4bit_grouped /
+ * gemm_mxfp4_grouped, reference kernel/nf4_grouped.py:750-806,
+ * kernel/mxfp4_grouped.py:146-160 (whose expert ids go through
+ * to_device_i32, kernel/nf4_grouped.py:229-331). */
+int gnf4_hip_grouped_decode_ids(int fmt, const void *a, int a_dtype, int64_t lda,
+                                const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                                const void *scales, int64_t stride_se, int64_t stride_sn,
+                                const int32_t *expert_ids, const int32_t *row_off, int G,
+                                int max_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                                void *stream);
 
 /* Grouped forward on 256-row tiles with the tile table in host memory: the
  * table (at most 256 m-tiles) travels in the kernel's arguments, so the call

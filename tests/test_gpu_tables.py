@@ -153,3 +153,50 @@ def test_kernel_argument_tables_in_graph_replays():
         want = op(a, W, S, sizes, ids)
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), r
+
+
+@pytest.mark.parametrize("fmt,K,sizes", [
+    ("nf4", 2048, [1] * 8), ("nf4", 768, [1] * 8), ("nf4", 2048, [1, 3, 2, 0, 4, 1]),
+    ("nf4", 768, [2, 1, 2, 1]), ("mxfp4", 2880, [1] * 4), ("nf4", 2048, [1, 8, 2]),
+])
+def test_kernel_argument_expert_ids_give_the_same_bits(fmt, K, sizes, monkeypatch):
+    """Decode calls with host ids pass them in the GEMV kernels' arguments;
+    the same calls with device ids (a table the kernel reads) and with the
+    argument path switched off give the same bits. The last case has a
+    group of 8 rows, which no GEMV class takes: it falls back to the tables."""
+    op, stack = _ops()[fmt]
+    E, N = 32, 320
+    W, S = stack(E, N, K, seed=31)
+    ids = [(7 * g + 3) % E for g in range(len(sizes))]
+    a = rand_acts(sum(sizes), K, seed=32)
+    got = op(a, W, S, sizes, ids)
+    dev_ids = op(a, W, S, sizes, torch.tensor(ids, dtype=torch.int32, device="cuda"))
+    monkeypatch.setattr(nf4_grouped, "IDS_ARG_MAX", 0)
+    want = op(a, W, S, sizes, ids)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(dev_ids.view(torch.int16), want.view(torch.int16))
+
+
+def test_kernel_argument_expert_ids_planned_and_many_groups(monkeypatch):
+    """launch_planned with host ids in the kernel arguments against the
+    device tables; and 400 one-row groups (more than the arguments hold),
+    which upload the tables: rows against single-group calls."""
+    op, stack = _ops()["nf4"]
+    E, N, K = 16, 256, 1024
+    W, S = stack(E, N, K, seed=33)
+    sizes, ids = [1, 2, 1, 1], [4, 15, 0, 9]
+    a = rand_acts(sum(sizes), K, seed=34)
+    plan = nf4_grouped.GroupPlan(sizes, ids, a.device)
+    got = nf4_grouped.launch_planned(0, a, W, S, plan)
+    monkeypatch.setattr(nf4_grouped, "IDS_ARG_MAX", 0)
+    want = nf4_grouped.launch_planned(0, a, W, S, plan)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    monkeypatch.undo()
+    G = 400
+    ids = [g % E for g in range(G)]
+    a = rand_acts(G, K, seed=35)
+    assert G > nf4_grouped.IDS_ARG_MAX
+    got = op(a, W, S, [1] * G, ids)
+    for g in (0, 7, 399):
+        one = op(a[g:g + 1], W, S, [1], [ids[g]])
+        assert torch.equal(got[g].view(torch.int16), one[0].view(torch.int16)), g

@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -37,6 +37,9 @@ SIGNATURES = {
     "gnf4_hip_nf4_ffn_fwd": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
                              _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P],
+    "gnf4_hip_nf4_ffn_decode_ids": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                    _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,
+                                    _I64, _I64, _I64, _P, _I64, _P, _I64, _P],
     "gnf4_hip_nf4_ffn_noalloc_reset": [_P, _P],
     "gnf4_hip_nf4_ffn_fwd_noalloc": [_P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                      _P, _I64, _I64, _P, _I64, _I64, _P, _P, _I, _I,

@@ -3816,17 +3816,28 @@ bool gemv_nf4_takes(const FwdArgs& p) {
   return has_ro && gemv_nf4_takes_rows(p.max_m, p.K);
 }
 
+// Whether launch_gemv<FMT> leaves p to another kernel class (returns 1
+// without launching anything).
 template <int FMT>
-int launch_gemv(const FwdArgs& p, hipStream_t stream) {
-  if (p.K <= 0 || p.K % (FMT == kNF4 ? 64 : 32) != 0 || p.N <= 0 || p.G <= 0) return 1;
+bool gemv_refuses(const FwdArgs& p) {
+  if (p.K <= 0 || p.K % (FMT == kNF4 ? 64 : 32) != 0 || p.N <= 0 || p.G <= 0) return true;
   const int64_t pr = p.K / 32;
   const int lr = gemv_slots<FMT>(pr);
   const int64_t ppl = (pr + lr - 1) / lr;
-  if (ppl > 4) return 1;
+  if (ppl > 4) return true;
   // 32-bit row offsets inside the expert's resources
   const int64_t sbytes = FMT == kNF4 ? 4 : 1;
-  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * sbytes > 0x7FFFFFFF) return 1;
-  if (p.max_m > 1 && (FMT != kNF4 || !gemv_nf4_takes(p))) return 1;
+  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * sbytes > 0x7FFFFFFF) return true;
+  if (p.max_m > 1 && (FMT != kNF4 || !gemv_nf4_takes(p) || ppl != 1)) return true;
+  return false;
+}
+
+template <int FMT>
+int launch_gemv(const FwdArgs& p, hipStream_t stream) {
+  if (gemv_refuses<FMT>(p)) return 1;
+  const int64_t pr = p.K / 32;
+  const int lr = gemv_slots<FMT>(pr);
+  const int64_t ppl = (pr + lr - 1) / lr;
   const int cus = device_cus();
   if (cus <= 0) return -2;
   // row steps per wave: about one workgroup per CU over the launch's rows
@@ -3834,8 +3845,7 @@ int launch_gemv(const FwdArgs& p, hipStream_t stream) {
   const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
   const int rpw = want <= 2 ? 2 : want <= 3 ? 3 : want <= 4 ? 4 : 6;
   if constexpr (FMT == kNF4) {
-    if (p.max_m > 1) {
-      if (ppl != 1) return 1;
+    if (p.max_m > 1) {   // ppl == 1 here
       if (lr == 32) return launch_gemv_rpw<FMT, 32, 1, true>(p, rpw, stream);
       return launch_gemv_rpw<FMT, 64, 1, true>(p, rpw, stream);
     }
@@ -4246,21 +4256,27 @@ int launch_gemv_gu_rpw(const FwdArgs& p, int64_t H, int rpw, hipStream_t stream)
 // gate_up stage of the expert FFN in the GEMV class: one-row groups, or
 // groups the multi-row GEMV takes (gemv_nf4_takes). Returns 1 when the
 // launch is not for it.
-int launch_gemv_gu(const FwdArgs& p, int64_t H, hipStream_t stream) {
+bool gemv_gu_refuses(const FwdArgs& p, int64_t H) {
   const int64_t pr = p.K / 32;
   const int lr = pr <= 32 ? 32 : 64;
   const int64_t ppl = (pr + lr - 1) / lr;
-  if (p.K % 64 || ppl > 4 || p.G > 65535) return 1;
-  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * 4 > 0x7FFFFFFF || H > 0x7FFFFFFF) return 1;
+  if (p.K <= 0 || p.K % 64 || ppl > 4 || p.G <= 0 || p.G > 65535) return true;
+  if (p.N * p.sbn > 0x7FFFFFFF || p.N * p.ssn * 4 > 0x7FFFFFFF || H > 0x7FFFFFFF) return true;
+  return p.max_m > 1 && (!gemv_nf4_takes(p) || ppl != 1);
+}
+
+int launch_gemv_gu(const FwdArgs& p, int64_t H, hipStream_t stream) {
+  if (gemv_gu_refuses(p, H)) return 1;
+  const int64_t pr = p.K / 32;
+  const int lr = pr <= 32 ? 32 : 64;
+  const int64_t ppl = (pr + lr - 1) / lr;
   const bool multi = p.max_m > 1;
-  if (multi && !gemv_nf4_takes(p)) return 1;
   const int cus = device_cus();
   if (cus <= 0) return -2;
   const int64_t per_step = (int64_t)cus * 8 * (64 / lr);
   const int64_t want = ((int64_t)p.G * p.N + per_step - 1) / per_step;
   const int rpw = want <= 2 ? 2 : want <= 4 ? 4 : 6;
-  if (multi) {
-    if (ppl != 1) return 1;
+  if (multi) {   // ppl == 1 here
     if (lr == 32) return launch_gemv_gu_rpw<32, 1, true>(p, H, rpw, stream);
     return launch_gemv_gu_rpw<64, 1, true>(p, H, rpw, stream);
   }
@@ -4586,6 +4602,78 @@ uint32_t* ffn_scratch_words() {
 
 }  // namespace
 
+namespace {
+
+// Copies host expert ids (and row offsets, when given) into a
+// kernel-argument table; false on a negative id or decreasing offsets.
+bool fill_gemv_ids(GemvIds& gi, const int32_t* expert_ids, const int32_t* row_off, int G) {
+  if (G < 1 || G > kGemvIdsMax || !expert_ids) return false;
+  for (int g = 0; g < G; ++g) {
+    if (expert_ids[g] < 0) return false;
+    gi.e[g] = expert_ids[g];
+  }
+  gi.has_ro = row_off ? 1 : 0;
+  if (row_off)
+    for (int g = 0; g <= G; ++g) {
+      if (row_off[g] < 0 || (g > 0 && row_off[g] < row_off[g - 1])) return false;
+      gi.ro[g] = row_off[g];
+    }
+  gi.n = G;
+  return true;
+}
+
+// Checks the fused expert FFN's arguments (all but the id tables and the
+// sync words) and fills the two stages' launch arguments; false on bad ones.
+bool ffn_stage_args(const void* a, int a_dtype, int64_t lda, const uint8_t* B_gu, int64_t gu_sbe,
+                    int64_t gu_sbn, const float* absmax_gu, int64_t gu_sae, int64_t gu_san,
+                    const uint8_t* B_dn, int64_t dn_sbe, int64_t dn_sbn, const float* absmax_dn,
+                    int64_t dn_sae, int64_t dn_san, bool has_row_off, int G, int max_m,
+                    int64_t N_gu, int64_t K, int64_t N_dn, void* h, int64_t ldh, void* out,
+                    int64_t ldo, FwdArgs& gu, FwdArgs& dn) {
+  if (a_dtype != GNF4_DTYPE_BF16) return false;
+  if (N_gu <= 0 || N_gu % 2 || (N_gu / 2) % 64 || K <= 0 || K % 64 || N_dn <= 0 || G < 0)
+    return false;
+  const int64_t H = N_gu / 2;
+  if (max_m < 1 || max_m > 16 || (!has_row_off && max_m != 1)) return false;
+  if (!a || !B_gu || !absmax_gu || !B_dn || !absmax_dn || !h || !out) return false;
+  if (lda < K || lda % 8 || ldh < H || ldh % 8 || ldo < N_dn || !aligned16(a) || !aligned16(h))
+    return false;
+  if (gu_sbn % 16 || gu_sbe % 16 || dn_sbn % 16 || dn_sbe % 16 || !aligned16(B_gu) ||
+      !aligned16(B_dn))
+    return false;
+  gu = FwdArgs{};
+  gu.a = static_cast<const uint16_t*>(a);
+  gu.lda = lda;
+  gu.B = B_gu;
+  gu.sbe = gu_sbe;
+  gu.sbn = gu_sbn;
+  gu.S = absmax_gu;
+  gu.sse = gu_sae;
+  gu.ssn = gu_san;
+  gu.G = G;
+  gu.max_m = max_m;
+  gu.N = N_gu;
+  gu.K = K;
+  gu.out = static_cast<uint16_t*>(h);
+  gu.ldo = ldh;
+  dn = gu;
+  dn.a = static_cast<const uint16_t*>(h);
+  dn.lda = ldh;
+  dn.B = B_dn;
+  dn.sbe = dn_sbe;
+  dn.sbn = dn_sbn;
+  dn.S = absmax_dn;
+  dn.sse = dn_sae;
+  dn.ssn = dn_san;
+  dn.N = N_dn;
+  dn.K = H;
+  dn.out = static_cast<uint16_t*>(out);
+  dn.ldo = ldo;
+  return true;
+}
+
+}  // namespace
+
 // ============================================================== C ABI ====
 
 extern "C" {
@@ -4684,52 +4772,19 @@ int gnf4_hip_nf4_ffn_fwd(const void* a, int a_dtype, int64_t lda, const uint8_t*
                          int G, int max_m, int64_t N_gu, int64_t K, int64_t N_dn, void* h,
                          int64_t ldh, uint32_t* sync, int64_t sync_words, void* out,
                          int64_t ldo, void* stream) {
-  if (a_dtype != GNF4_DTYPE_BF16) return -1;
-  if (N_gu <= 0 || N_gu % 2 || (N_gu / 2) % 64 || K <= 0 || K % 64 || N_dn <= 0 || G < 0)
+  FwdArgs gu, dn;
+  if (!ffn_stage_args(a, a_dtype, lda, B_gu, gu_sbe, gu_sbn, absmax_gu, gu_sae, gu_san, B_dn,
+                      dn_sbe, dn_sbn, absmax_dn, dn_sae, dn_san, row_off != nullptr, G, max_m,
+                      N_gu, K, N_dn, h, ldh, out, ldo, gu, dn))
     return -1;
-  const int64_t H = N_gu / 2;
-  if (max_m < 1 || max_m > 16 || (!row_off && max_m != 1)) return -1;
-  if (!a || !B_gu || !absmax_gu || !B_dn || !absmax_dn || !expert_ids || !h || !sync || !out)
-    return -1;
-  if (lda < K || lda % 8 || ldh < H || ldh % 8 || ldo < N_dn || !aligned16(a) || !aligned16(h))
-    return -1;
-  if (gu_sbn % 16 || gu_sbe % 16 || dn_sbn % 16 || dn_sbe % 16 || !aligned16(B_gu) ||
-      !aligned16(B_dn))
-    return -1;
+  if (!expert_ids || !sync) return -1;
   if (sync_words < gnf4_hip_ffn_sync_words(G, N_gu, N_dn) ||
       ((reinterpret_cast<uintptr_t>(sync) & 3) != 0))
     return -1;
   if (G == 0) return 0;
-  FwdArgs gu{};
-  gu.a = static_cast<const uint16_t*>(a);
-  gu.lda = lda;
-  gu.B = B_gu;
-  gu.sbe = gu_sbe;
-  gu.sbn = gu_sbn;
-  gu.S = absmax_gu;
-  gu.sse = gu_sae;
-  gu.ssn = gu_san;
-  gu.eids = expert_ids;
-  gu.row_off = row_off;
-  gu.G = G;
-  gu.max_m = max_m;
-  gu.N = N_gu;
-  gu.K = K;
-  gu.out = static_cast<uint16_t*>(h);
-  gu.ldo = ldh;
-  FwdArgs dn = gu;
-  dn.a = static_cast<const uint16_t*>(h);
-  dn.lda = ldh;
-  dn.B = B_dn;
-  dn.sbe = dn_sbe;
-  dn.sbn = dn_sbn;
-  dn.S = absmax_dn;
-  dn.sse = dn_sae;
-  dn.ssn = dn_san;
-  dn.N = N_dn;
-  dn.K = H;
-  dn.out = static_cast<uint16_t*>(out);
-  dn.ldo = ldo;
+  const int64_t H = N_gu / 2;
+  gu.eids = dn.eids = expert_ids;
+  gu.row_off = dn.row_off = row_off;
   if (device_cus() <= 0) return -2;
   const FfnSync fs{sync, next_ffn_epoch(), g_ffn_spin_limit.load(std::memory_order_relaxed)};
   return launch_ffn(gu, dn, H, fs, static_cast<hipStream_t>(stream));
@@ -4751,6 +4806,36 @@ int gnf4_hip_nf4_ffn_fwd_noalloc(const void* a, int a_dtype, int64_t lda, const 
                               B_dn, dn_sbe, dn_sbn, absmax_dn, dn_sae, dn_san, expert_ids,
                               row_off, G, max_m, N_gu, K, N_dn, h, ldh, words,
                               kFfnScratchWords, out, ldo, stream);
+}
+
+int gnf4_hip_nf4_ffn_decode_ids(const void* a, int a_dtype, int64_t lda, const uint8_t* B_gu,
+                                int64_t gu_sbe, int64_t gu_sbn, const float* absmax_gu,
+                                int64_t gu_sae, int64_t gu_san, const uint8_t* B_dn,
+                                int64_t dn_sbe, int64_t dn_sbn, const float* absmax_dn,
+                                int64_t dn_sae, int64_t dn_san, const int32_t* expert_ids,
+                                const int32_t* row_off, int G, int max_m, int64_t N_gu,
+                                int64_t K, int64_t N_dn, void* h, int64_t ldh, void* out,
+                                int64_t ldo, void* stream) {
+  FwdArgs gu, dn;
+  if (!ffn_stage_args(a, a_dtype, lda, B_gu, gu_sbe, gu_sbn, absmax_gu, gu_sae, gu_san, B_dn,
+                      dn_sbe, dn_sbn, absmax_dn, dn_sae, dn_san, row_off != nullptr, G, max_m,
+                      N_gu, K, N_dn, h, ldh, out, ldo, gu, dn))
+    return -1;
+  if (G == 0) return 0;
+  if (!expert_ids) return -1;
+  if (G > kGemvIdsMax) return 1;   // the caller takes the device-table entry
+  GemvIds gi;
+  if (!fill_gemv_ids(gi, expert_ids, row_off, G)) return -1;
+  const int64_t H = N_gu / 2;
+  gu.ids_inline = dn.ids_inline = &gi;
+  // both stages must be GEMV launches (the only kernels that read
+  // kernel-argument ids): decided before anything is launched
+  if (gemv_gu_refuses(gu, H) || gemv_refuses<kNF4>(dn)) return 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int r1 = launch_gemv_gu(gu, H, s);
+  if (r1 != 0) return r1 < 0 ? r1 : -2;
+  const int r2 = launch_gemv<kNF4>(dn, s);
+  return r2 == 0 ? 0 : r2 < 0 ? r2 : -2;
 }
 
 int gnf4_hip_nf4_ffn_noalloc_reset(uint32_t* error_word, void* stream) {
@@ -4845,17 +4930,7 @@ int gnf4_hip_grouped_decode_ids(int fmt, const void* a, int a_dtype, int64_t lda
       !aligned16(a))
     return -1;
   GemvIds gi;
-  for (int g = 0; g < G; ++g) {
-    if (expert_ids[g] < 0) return -1;
-    gi.e[g] = expert_ids[g];
-  }
-  gi.has_ro = row_off ? 1 : 0;
-  if (row_off)
-    for (int g = 0; g <= G; ++g) {
-      if (row_off[g] < 0 || (g > 0 && row_off[g] < row_off[g - 1])) return -1;
-      gi.ro[g] = row_off[g];
-    }
-  gi.n = G;
+  if (!fill_gemv_ids(gi, expert_ids, row_off, G)) return -1;
   FwdArgs p{};
   p.a = static_cast<const uint16_t*>(a);
   p.lda = lda;

@@ -33,6 +33,8 @@ from __future__ import annotations
 
 import threading
 
+import numpy as np
+
 import torch
 
 import _hiplib
@@ -239,6 +241,15 @@ def gemm_nf4_ffn_grouped(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, size
         h = silu_mul_locked(gu)
         return nf4_grouped.gemm_4bit_grouped(h, dn_packed, dn_absmax, sizes, expert_ids)
     a = _bf16_activations(a_cat, "gemm_nf4_ffn_grouped")
+    if eids_dev is None and G <= nf4_grouped.IDS_ARG_MAX:
+        ro = None
+        if not (min(sizes_i) == 1 and max_m == 1):
+            ro = np.zeros(G + 1, dtype=np.int32)
+            np.cumsum(np.asarray(sizes_i, dtype=np.int32), out=ro[1:])
+        out = _launch_fused_ids(a, gu_packed, gu_absmax, dn_packed, dn_absmax,
+                                nf4_grouped._np_ids(expert_ids), ro, G, max_m)
+        if out is not None:
+            return out
     row_off = [0]
     for m in sizes_i:
         row_off.append(row_off[-1] + m)
@@ -280,6 +291,37 @@ def _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, eids, row_off, 
     return out
 
 
+def _launch_fused_ids(a, gu_packed, gu_absmax, dn_packed, dn_absmax, ids32, row_off, G: int,
+                      max_m: int, h=None, out=None, op="gemm_nf4_ffn_grouped"):
+    """The fused FFN with host group tables (``ids32 [G]``, ``row_off
+    [G + 1]`` or None for one row per group, int32 numpy) passed in the
+    kernels' arguments (``gnf4_hip_nf4_ffn_decode_ids``): no upload and no
+    table read ahead of the weights. None when the library leaves the call to
+    the device-table entry (a stage that is not a GEMV launch, or G above its
+    table size)."""
+    T, K = a.shape
+    H, n_dn = gu_packed.shape[1] // 2, dn_packed.shape[1]
+    dev = a.device
+    Wg, Sg = _aligned_rows(gu_packed, 16), _scales_view(gu_absmax)
+    Wd, Sd = _aligned_rows(dn_packed, 16), _scales_view(dn_absmax)
+    if h is None:
+        h = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty(T, n_dn, dtype=torch.bfloat16, device=dev)
+    with nf4_grouped._device_ctx(dev):
+        rc = _hiplib.load().gnf4_hip_nf4_ffn_decode_ids(
+            a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
+            Wg.data_ptr(), Wg.stride(0), Wg.stride(1), Sg.data_ptr(), Sg.stride(0), Sg.stride(1),
+            Wd.data_ptr(), Wd.stride(0), Wd.stride(1), Sd.data_ptr(), Sd.stride(0), Sd.stride(1),
+            ids32.ctypes.data, row_off.ctypes.data if row_off is not None else None, G,
+            max(max_m, 1), 2 * H, K, n_dn, h.data_ptr(), h.stride(0),
+            out.data_ptr(), out.stride(0), _stream_ptr(dev))
+    if rc == 1:
+        return None
+    _hiplib.check(rc, op)
+    return out
+
+
 def launch_ffn_planned(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, plan, h=None,
                        out=None):
     """Fused FFN launch with a prepared decode ``nf4_grouped.GroupPlan``: the
@@ -293,6 +335,12 @@ def launch_ffn_planned(a_cat, gu_packed, gu_absmax, dn_packed, dn_absmax, plan, 
     if plan.min_id < 0 or plan.max_id >= E:
         raise ValueError(f"expert id out of range [0, {E})")
     a = _bf16_activations(a_cat, "launch_ffn_planned")
+    if 0 < plan.G <= nf4_grouped.IDS_ARG_MAX:
+        res = _launch_fused_ids(a, gu_packed, gu_absmax, dn_packed, dn_absmax, plan.host_ids,
+                                plan.host_row_off, plan.G, plan.max_m, h=h, out=out,
+                                op="launch_ffn_planned")
+        if res is not None:
+            return res
     return _launch_fused(a, gu_packed, gu_absmax, dn_packed, dn_absmax, plan.eids, plan.row_off,
                          plan.G, plan.max_m, h=h, out=out, op="launch_ffn_planned")
 

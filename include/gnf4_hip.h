@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 11
+#define GNF4_HIP_ABI_VERSION 12
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -272,6 +272,27 @@ int gnf4_hip_nf4_ffn_fwd_noalloc(const void *a, int a_dtype, int64_t lda,
                                  const int32_t *expert_ids, const int32_t *row_off, int G,
                                  int max_m, int64_t N_gu, int64_t K, int64_t N_dn, void *h,
                                  int64_t ldh, void *out, int64_t ldo, void *stream);
+
+/* gnf4_hip_nf4_ffn_fwd with host group tables: expert_ids [G] and row_off
+ * [G + 1] (NULL when every group is one row) are host int32 arrays, copied
+ * into the kernels' arguments, so nothing is uploaded and the kernels read
+ * no table ahead of the weights. Runs only when both stages are GEMV
+ * launches (groups of one row; or, with row_off, groups of at most 4 rows
+ * at 1024 < K <= 2048 and 2 at K <= 1024 for each stage's K) and
+ * G <= 384; otherwise returns 1 before launching anything and the caller
+ * takes gnf4_hip_nf4_ffn_fwd. Same bits as gnf4_hip_nf4_ffn_fwd; no sync
+ * words. Same operation as the reference's CPU gnf4_gemv_nf4_ffn_grouped
+ * (gnf4_native/cpu_kernels.c:948-986), whose ids are host arrays too. 0 on
+ * success, -1 on bad arguments (a negative id, decreasing offsets), -2 on a
+ * runtime error. */
+int gnf4_hip_nf4_ffn_decode_ids(const void *a, int a_dtype, int64_t lda, const uint8_t *B_gu,
+                                int64_t gu_sbe, int64_t gu_sbn, const float *absmax_gu,
+                                int64_t gu_sae, int64_t gu_san, const uint8_t *B_dn,
+                                int64_t dn_sbe, int64_t dn_sbn, const float *absmax_dn,
+                                int64_t dn_sae, int64_t dn_san, const int32_t *expert_ids,
+                                const int32_t *row_off, int G, int max_m, int64_t N_gu,
+                                int64_t K, int64_t N_dn, void *h, int64_t ldh, void *out,
+                                int64_t ldo, void *stream);
 
 /* Stream-ordered read and clear of the fixed sync array of
  * gnf4_hip_nf4_ffn_fwd_noalloc on the current device: copies its error word

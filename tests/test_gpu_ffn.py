@@ -377,3 +377,99 @@ def test_fused_hand_off_soak_in_graph_replays(B):
         if not torch.equal(_bits(out), _bits(want[i])):
             pytest.fail(f"replay {r} (activations {i}) differs from the composition")
     assert not nf4_ffn.ffn_sync_error()
+
+
+# ------------------------------------------- kernel-argument group tables --
+
+@pytest.mark.parametrize("sizes", [
+    [1] * 8,                 # batch 1, top-8: no offset table
+    [2, 1, 2, 1],            # multi-row groups both stages' GEMVs take
+    [1, 0, 1, 0, 1],         # empty groups (offset table, one-row GEMV)
+])
+def test_kernel_argument_tables_give_the_device_table_bits(sizes):
+    nf4_ffn, nf4_grouped = _mods()
+    gu_p, gu_a, dn_p, dn_a = _stack(QWEN["E"], QWEN["H"], QWEN["K"], QWEN["N_dn"], seed=21)
+    G = len(sizes)
+    ids = [(37 * g + 5) % QWEN["E"] for g in range(G)]
+    a = rand_acts(sum(sizes), QWEN["K"], seed=22)
+    ro = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    one_row = min(sizes) == 1 and max(sizes) == 1
+    out = nf4_ffn._launch_fused_ids(a, gu_p, gu_a, dn_p, dn_a, np.asarray(ids, np.int32),
+                                    None if one_row else ro, G, max(sizes))
+    assert out is not None
+    e_d = torch.tensor(ids, dtype=torch.int32, device="cuda")
+    r_d = torch.from_numpy(ro).cuda()
+    ref = nf4_ffn._launch_fused(a, gu_p, gu_a, dn_p, dn_a, e_d, r_d, G, max(sizes))
+    assert torch.equal(_bits(out), _bits(ref))
+    assert torch.equal(_bits(out), _bits(_composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)))
+
+
+def test_kernel_argument_tables_refuse_before_launching():
+    nf4_ffn, _ = _mods()
+    gu_p, gu_a, dn_p, dn_a = _stack(QWEN["E"], QWEN["H"], QWEN["K"], QWEN["N_dn"], seed=23)
+    # 3 rows: the down stage (K = 768) is no GEMV launch; the call returns
+    # before launching, so the output buffer keeps its sentinel
+    sizes, ids = [3, 1], [4, 9]
+    a = rand_acts(4, QWEN["K"], seed=24)
+    out = torch.full((4, QWEN["N_dn"]), 7.0, dtype=torch.bfloat16, device="cuda")
+    ro = np.asarray([0, 3, 4], np.int32)
+    assert nf4_ffn._launch_fused_ids(a, gu_p, gu_a, dn_p, dn_a, np.asarray(ids, np.int32), ro,
+                                     2, 3, out=out) is None
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    # the op then takes the device-table launch: same bits as the chain
+    got = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
+    assert torch.equal(_bits(got), _bits(_composed(a, gu_p, gu_a, dn_p, dn_a, sizes, ids)))
+
+
+@pytest.mark.parametrize("G", [384, 385])
+def test_kernel_argument_tables_at_and_past_their_size(G):
+    nf4_ffn, _ = _mods()
+    E, H, K, N_dn = 16, 64, 128, 64
+    gu_p, gu_a, dn_p, dn_a = _stack(E, H, K, N_dn, seed=25)
+    sizes, ids = [1] * G, [(7 * g) % E for g in range(G)]
+    a = rand_acts(G, K, seed=26)
+    got = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, ids, fused=True)
+    dev_ids = torch.tensor(ids, device="cuda")
+    ref = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes, dev_ids, fused=True)
+    assert torch.equal(_bits(got), _bits(ref))
+
+
+def test_kernel_argument_tables_planned_in_a_graph():
+    nf4_ffn, nf4_grouped = _mods()
+    gu_p, gu_a, dn_p, dn_a = _stack(QWEN["E"], QWEN["H"], QWEN["K"], QWEN["N_dn"], seed=27)
+    sizes, ids = [1] * 8, [3, 17, 40, 41, 77, 90, 101, 127]
+    a = rand_acts(8, QWEN["K"], seed=28)
+    plan = nf4_grouped.GroupPlan(sizes, ids, "cuda")
+    h = torch.empty(8, QWEN["H"], dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(8, QWEN["N_dn"], dtype=torch.bfloat16, device="cuda")
+    want = nf4_ffn.gemm_nf4_ffn_grouped(a, gu_p, gu_a, dn_p, dn_a, sizes,
+                                        torch.tensor(ids, device="cuda"), fused=True)
+    nf4_ffn.launch_ffn_planned(a, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out), _bits(want))
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            nf4_ffn.launch_ffn_planned(a, gu_p, gu_a, dn_p, dn_a, plan, h=h, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(out), _bits(want))
+
+
+def test_kernel_argument_tables_reject_bad_ids():
+    nf4_ffn, _ = _mods()
+    gu_p, gu_a, dn_p, dn_a = _stack(8, 64, 128, 64, seed=29)
+    a = rand_acts(2, 128, seed=30)
+    with pytest.raises(ValueError):
+        nf4_ffn._launch_fused_ids(a, gu_p, gu_a, dn_p, dn_a, np.asarray([1, -1], np.int32),
+                                  None, 2, 1)
+    with pytest.raises(ValueError):   # decreasing offsets
+        nf4_ffn._launch_fused_ids(a, gu_p, gu_a, dn_p, dn_a, np.asarray([1, 2], np.int32),
+                                  np.asarray([0, 2, 1], np.int32), 2, 1)

@@ -695,10 +695,10 @@ def main():
         # config 2's batch sweep over the model's layers (their own bytes: at
         # batch 1 a graph of fewer layers could sit in the 256 MB Infinity Cache)
         sweep = {}
-        for b in (1, 4, 16):
+        for b in (1, 2, 4, 8, 16):
             m = DecodeModel("nf4", QWEN, b, dev, seed=b, layers=model.L, weights=(model.gu, model.dn))
             sweep[f"b{b}"] = decode_report(m)
-            if b > 1:
+            if b in (4, 16):
                 extra[f"qwen3_nf4_ffn_b{b}"] = ffn_report(m)
             del m
         extra["qwen3_nf4_decode_sweep"] = sweep

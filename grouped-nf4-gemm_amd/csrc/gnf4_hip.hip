@@ -330,15 +330,20 @@ struct FwdArgs {
   const struct GemvIds* ids_inline;
 };
 
-// The expert ids (and row offsets) of a decode launch of at most
-// kGemvIdsMax groups, in the GEMV kernels' arguments (n > 0): the kernel
-// reads them from the kernarg segment it loads anyway, instead of a table
-// in memory behind it (one dependent round trip before the first weight
-// load). ro holds G + 1 offsets when has_ro, else group g is row g.
+// The groups of a decode launch of at most kGemvIdsMax groups, in the GEMV
+// kernels' arguments (n > 0): the kernel reads them from the kernarg
+// segment it loads anyway, instead of a table in memory behind it (one
+// dependent round trip before the first weight load). Entry y (grid row y)
+// is a group: its expert id e[y] and rows[y] = first row << 8 | row count.
+// The host lists the groups largest first, so the workgroups of the groups
+// that take the most passes are dispatched first (every output row is
+// computed on its own: the order changes no bits). has_ro: the caller gave
+// row offsets (the multi-row GEMV needs them).
 constexpr int kGemvIdsMax = 384;
+constexpr int kGemvRowsMax = 1 << 23;   // first rows must fit in rows[y] >> 8
 struct GemvIds {
   int32_t e[kGemvIdsMax];
-  int32_t ro[kGemvIdsMax + 1];
+  int32_t rows[kGemvIdsMax];
   int32_t n;
   int32_t has_ro;
 };
@@ -1006,11 +1011,10 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   // kernel-argument ids: loaded with the other arguments, in one round trip
   // (a clamped index keeps every load inside the arguments)
   const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
-  const int gi_n = gi.n, gi_ro = gi.has_ro, gi_e = gi.e[gc], gi_r0 = gi.ro[gc],
-            gi_r1 = gi.ro[gc + 1];
+  const int gi_n = gi.n, gi_e = gi.e[gc], gi_rows = gi.rows[gc];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
                "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
-               "s"(q.ldo), "s"(gi_n), "s"(gi_ro), "s"(gi_e), "s"(gi_r0), "s"(gi_r1));
+               "s"(q.ldo), "s"(gi_n), "s"(gi_e), "s"(gi_rows));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
   const int g = (int)blockIdx.y;
@@ -1018,10 +1022,10 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   int e32, ro_a, ro_b;
   bool has_ro;
   if (gi_n > 0) {   // ids in the kernel arguments
-    has_ro = gi_ro != 0;
+    has_ro = true;
     e32 = gi_e;
-    ro_a = has_ro ? gi_r0 : 0;
-    ro_b = has_ro ? gi_r1 : 1;
+    ro_a = gi_rows >> 8;
+    ro_b = ro_a + (gi_rows & 0xFF);
   } else {
     has_ro = q.row_off != nullptr;
     const int32_t* ce = q.eids + g;
@@ -1181,21 +1185,20 @@ __global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p, const GemvI
   // kernel-argument ids: loaded with the other arguments, in one round trip
   // (a clamped index keeps every load inside the arguments)
   const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
-  const int gi_n = gi.n, gi_ro = gi.has_ro, gi_e = gi.e[gc], gi_r0 = gi.ro[gc],
-            gi_r1 = gi.ro[gc + 1];
+  const int gi_n = gi.n, gi_e = gi.e[gc], gi_rows = gi.rows[gc];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
                "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
-               "s"(q.ldo), "s"(gi_n), "s"(gi_ro), "s"(gi_e), "s"(gi_r0), "s"(gi_r1));
+               "s"(q.ldo), "s"(gi_n), "s"(gi_e), "s"(gi_rows));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
   const int g = (int)blockIdx.y;
   int e32, ro_a, ro_b;
   bool has_ro;
   if (gi_n > 0) {   // ids in the kernel arguments
-    has_ro = gi_ro != 0;
+    has_ro = true;
     e32 = gi_e;
-    ro_a = has_ro ? gi_r0 : 0;
-    ro_b = has_ro ? gi_r1 : 1;
+    ro_a = gi_rows >> 8;
+    ro_b = ro_a + (gi_rows & 0xFF);
   } else {
     has_ro = q.row_off != nullptr;
     const int32_t* ce = q.eids + g;
@@ -4604,22 +4607,39 @@ uint32_t* ffn_scratch_words() {
 
 namespace {
 
-// Copies host expert ids (and row offsets, when given) into a
-// kernel-argument table; false on a negative id or decreasing offsets.
-bool fill_gemv_ids(GemvIds& gi, const int32_t* expert_ids, const int32_t* row_off, int G) {
-  if (G < 1 || G > kGemvIdsMax || !expert_ids) return false;
+// Copies host expert ids (and row offsets, when given; else group g is row
+// g) into a kernel-argument table, largest groups first (a stable counting
+// sort on the row count). 0 on success, -1 on a negative id or decreasing
+// offsets, 1 when a group does not fit an entry (more than 255 rows, or a
+// first row past kGemvRowsMax): the caller then takes the device tables.
+int fill_gemv_ids(GemvIds& gi, const int32_t* expert_ids, const int32_t* row_off, int G) {
+  if (G < 1 || G > kGemvIdsMax || !expert_ids) return -1;
+  int cnt[kGemvIdsMax], first[kGemvIdsMax];
   for (int g = 0; g < G; ++g) {
-    if (expert_ids[g] < 0) return false;
-    gi.e[g] = expert_ids[g];
+    if (expert_ids[g] < 0) return -1;
+    if (row_off) {
+      if (row_off[g] < 0 || row_off[g + 1] < row_off[g]) return -1;
+      cnt[g] = row_off[g + 1] - row_off[g];
+      first[g] = row_off[g];
+    } else {
+      cnt[g] = 1;
+      first[g] = g;
+    }
+  }
+  for (int g = 0; g < G; ++g)
+    if (cnt[g] > 255 || first[g] >= kGemvRowsMax) return 1;
+  // bucket k = 255 - rows: start[k] = how many groups have more rows
+  int start[257] = {};
+  for (int g = 0; g < G; ++g) ++start[255 - cnt[g] + 1];
+  for (int k = 1; k <= 256; ++k) start[k] += start[k - 1];
+  for (int g = 0; g < G; ++g) {
+    const int y = start[255 - cnt[g]]++;
+    gi.e[y] = expert_ids[g];
+    gi.rows[y] = first[g] << 8 | cnt[g];
   }
   gi.has_ro = row_off ? 1 : 0;
-  if (row_off)
-    for (int g = 0; g <= G; ++g) {
-      if (row_off[g] < 0 || (g > 0 && row_off[g] < row_off[g - 1])) return false;
-      gi.ro[g] = row_off[g];
-    }
   gi.n = G;
-  return true;
+  return 0;
 }
 
 // Checks the fused expert FFN's arguments (all but the id tables and the
@@ -4825,7 +4845,8 @@ int gnf4_hip_nf4_ffn_decode_ids(const void* a, int a_dtype, int64_t lda, const u
   if (!expert_ids) return -1;
   if (G > kGemvIdsMax) return 1;   // the caller takes the device-table entry
   GemvIds gi;
-  if (!fill_gemv_ids(gi, expert_ids, row_off, G)) return -1;
+  const int fill = fill_gemv_ids(gi, expert_ids, row_off, G);
+  if (fill != 0) return fill;
   const int64_t H = N_gu / 2;
   gu.ids_inline = dn.ids_inline = &gi;
   // both stages must be GEMV launches (the only kernels that read
@@ -4930,7 +4951,8 @@ int gnf4_hip_grouped_decode_ids(int fmt, const void* a, int a_dtype, int64_t lda
       !aligned16(a))
     return -1;
   GemvIds gi;
-  if (!fill_gemv_ids(gi, expert_ids, row_off, G)) return -1;
+  const int fill = fill_gemv_ids(gi, expert_ids, row_off, G);
+  if (fill != 0) return fill;
   FwdArgs p{};
   p.a = static_cast<const uint16_t*>(a);
   p.lda = lda;

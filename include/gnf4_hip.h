@@ -118,9 +118,11 @@ int gnf4_hip_grouped_fwd(int fmt, const void *a, int a_dtype, int64_t lda,
  * upload, and a captured call is the kernel node alone. Same bits as
  * gnf4_hip_grouped_fwd's decode path with the same ids. expert_ids[G] and
  * row_off[G + 1] (NULL: group g is row g, max_m = 1) are read before the
- * call returns. Returns 1, launching nothing, when G > 384 or no GEMV class
- * takes the launch (the caller then uploads the tables and calls
- * gnf4_hip_grouped_fwd). Replaces the decode launches of gemm_4bit_grouped /
+ * call returns. The kernel's grid takes the groups largest first (the
+ * workgroups that make the most passes start first; no bits change).
+ * Returns 1, launching nothing, when G > 384, a group has more than 255
+ * rows or starts past row 2^23, or no GEMV class takes the launch (the
+ * caller then uploads the tables and calls gnf4_hip_grouped_fwd). Replaces the decode launches of gemm_4bit_grouped /
  * gemm_mxfp4_grouped, reference kernel/nf4_grouped.py:750-806,
  * kernel/mxfp4_grouped.py:146-160 (whose expert ids go through
  * to_device_i32, kernel/nf4_grouped.py:229-331). */

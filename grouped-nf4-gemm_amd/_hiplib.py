@@ -12,7 +12,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libgnf4_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 FMT_NF4 = 0
 FMT_MXFP4 = 1
@@ -53,6 +53,8 @@ SIGNATURES = {
     "gnf4_hip_grouped_fwd": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                              _P, _P, _I, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_decode_ids": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
+                                    _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
+    "gnf4_hip_grouped_decode_pairs": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                     _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],
     "gnf4_hip_grouped_fwd_tiles": [_I, _P, _I, _I64, _P, _I64, _I64, _P, _I64, _I64,
                                    _P, _P, _P, _P, _I, _I, _I64, _I64, _P, _I64, _P],

@@ -315,13 +315,18 @@ struct FwdArgs {
   const void* S;            // absmax f32 [E, N, K/64] or e8m0 u8 [E, N, K/32]
   int64_t sse, ssn;         // elements
   const int32_t* eids;      // [G]
-  const int32_t* row_off;   // [G + 1], or null: group g is the single row g
+  const int32_t* row_off;   // [G + 1] (ro_shift 0), [2 G] (ro_shift 1), or
+                            // null: group g is the single row g
   const int32_t* t_row0;    // [n_mtiles] (gemm path)
   const int32_t* t_rows;
   const int32_t* t_group;
   int n_mtiles;
   int G;
   int max_m;                // largest group (decode path)
+  // decode path: group g's rows are [row_off[g << ro_shift],
+  // row_off[(g << ro_shift) + 1]): ro_shift 0 reads the G + 1 prefix offsets,
+  // 1 a (first, end) pair per group, so the groups may come in any order
+  int ro_shift;
   int64_t N, K;
   uint16_t* out;            // [T, ldo] bf16
   int64_t ldo;
@@ -563,7 +568,7 @@ __device__ __forceinline__ void decode_unit(const FwdArgs& p, const int g, const
   // (their latency heads every weight load): a null row_off reads the id
   // twice instead of branching
   const int32_t* ce = p.eids + g;
-  const int32_t* cr = p.row_off ? p.row_off + g : ce;
+  const int32_t* cr = p.row_off ? p.row_off + (g << p.ro_shift) : ce;
   const int32_t* cr1 = p.row_off ? cr + 1 : ce;
   const int one = p.row_off ? 1 : 0;
   int e32, ro_a, ro_b;
@@ -944,7 +949,7 @@ __global__ void __launch_bounds__(64 * kDecodeWaves, kDecodeWaves / 2) k_decode_
   // each behind a branch)
   const FwdArgs q = p;
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
-               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.ro_shift), "s"(q.N), "s"(q.K), "s"(q.out),
                "s"(q.ldo));
   const int g = (int)blockIdx.y;   // < G: the grid has exactly G rows of units
   decode_unit<FMT, kChunksPerWave, kTiles, kDecodeWaves, kAPieces, kPlain, kSets>(
@@ -1013,7 +1018,7 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
   const int gi_n = gi.n, gi_e = gi.e[gc], gi_rows = gi.rows[gc];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
-               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.ro_shift), "s"(q.N), "s"(q.K), "s"(q.out),
                "s"(q.ldo), "s"(gi_n), "s"(gi_e), "s"(gi_rows));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
@@ -1029,7 +1034,7 @@ __global__ void __launch_bounds__(512, PPL >= 3 ? 1 : 2) k_gemv_nf4(const FwdArg
   } else {
     has_ro = q.row_off != nullptr;
     const int32_t* ce = q.eids + g;
-    const int32_t* cr = has_ro ? q.row_off + g : ce;
+    const int32_t* cr = has_ro ? q.row_off + (g << q.ro_shift) : ce;
     const int32_t* cr1 = has_ro ? cr + 1 : ce;
     asm volatile(
         "s_load_dword %0, %3, 0x0\n\t"
@@ -1187,7 +1192,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p, const GemvI
   const int gc = (int)blockIdx.y < kGemvIdsMax ? (int)blockIdx.y : kGemvIdsMax - 1;
   const int gi_n = gi.n, gi_e = gi.e[gc], gi_rows = gi.rows[gc];
   asm volatile("" ::"s"(q.a), "s"(q.lda), "s"(q.B), "s"(q.sbe), "s"(q.sbn), "s"(q.S), "s"(q.sse),
-               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.N), "s"(q.K), "s"(q.out),
+               "s"(q.ssn), "s"(q.eids), "s"(q.row_off), "s"(q.ro_shift), "s"(q.N), "s"(q.K), "s"(q.out),
                "s"(q.ldo), "s"(gi_n), "s"(gi_e), "s"(gi_rows));
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rl = lane / LR, j = lane % LR;
@@ -1202,7 +1207,7 @@ __global__ void __launch_bounds__(512, 2) k_gemv_mx(const FwdArgs p, const GemvI
   } else {
     has_ro = q.row_off != nullptr;
     const int32_t* ce = q.eids + g;
-    const int32_t* cr = has_ro ? q.row_off + g : ce;
+    const int32_t* cr = has_ro ? q.row_off + (g << q.ro_shift) : ce;
     const int32_t* cr1 = has_ro ? cr + 1 : ce;
     asm volatile(
         "s_load_dword %0, %3, 0x0\n\t"
@@ -1323,7 +1328,7 @@ __global__ void __launch_bounds__(64 * kW, 4) k_decode_rows(const FwdArgs p) {
   const int g = (int)blockIdx.y;
 
   const int32_t* ce = p.eids + g;
-  const int32_t* cr = p.row_off ? p.row_off + g : ce;
+  const int32_t* cr = p.row_off ? p.row_off + (g << p.ro_shift) : ce;
   const int32_t* cr1 = p.row_off ? cr + 1 : ce;
   const int one = p.row_off ? 1 : 0;
   int e32, ro_a, ro_b;
@@ -1613,7 +1618,8 @@ __global__ void __launch_bounds__(512, 1)
       "s_load_dword %2, %5, 0x0\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
-      : "s"(p.eids + g), "s"(p.row_off + g), "s"(p.row_off + g + 1)
+      : "s"(p.eids + g), "s"(p.row_off + (g << p.ro_shift)),
+        "s"(p.row_off + (g << p.ro_shift) + 1)
       : "memory");
   const int64_t e = e32;
   const int r0 = ro_a;
@@ -1833,7 +1839,8 @@ __global__ void __launch_bounds__(1024, 1)
       "s_load_dword %2, %5, 0x0\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(e32), "=&s"(ro_a), "=&s"(ro_b)
-      : "s"(p.eids + g), "s"(p.row_off + g), "s"(p.row_off + g + 1)
+      : "s"(p.eids + g), "s"(p.row_off + (g << p.ro_shift)),
+        "s"(p.row_off + (g << p.ro_shift) + 1)
       : "memory");
   const int64_t e = e32;
   const int r0 = ro_a;
@@ -2024,7 +2031,8 @@ __global__ void __launch_bounds__(512, 4) k_ffn_decode(const FwdArgs gu, const F
   }
   const int64_t d = u - gu_units;
   const int g = (int)((uint32_t)d / (uint32_t)dn_per_group);
-  const int M = dn.row_off ? dn.row_off[g + 1] - dn.row_off[g] : 1;
+  const int32_t* ro = dn.row_off ? dn.row_off + (g << dn.ro_shift) : nullptr;
+  const int M = ro ? ro[1] - ro[0] : 1;
   if (M <= 0) return;                   // empty group: no gate/up unit sets its flags
   uint32_t* row = sync + kFfnFlagBase + d * gu_per_group;
   auto wait_h = [&](int* status) {
@@ -4164,7 +4172,7 @@ int launch_decode(const FwdArgs& p, hipStream_t stream) {
     q.G = p.G - g0 < 65535 ? p.G - g0 : 65535;
     q.eids = p.eids + g0;
     if (p.row_off) {
-      q.row_off = p.row_off + g0;   // absolute row offsets
+      q.row_off = p.row_off + ((int64_t)g0 << p.ro_shift);   // absolute row offsets
     } else {                        // group g is row g
       q.a = p.a + (int64_t)g0 * p.lda;
       q.out = p.out + (int64_t)g0 * p.ldo;
@@ -4979,6 +4987,42 @@ int gnf4_hip_grouped_decode_ids(int fmt, const void* a, int a_dtype, int64_t lda
   }
   if (max_m > 1) return 1;
   return launch_gemv<kMX>(p, s);
+}
+
+int gnf4_hip_grouped_decode_pairs(int fmt, const void* a, int a_dtype, int64_t lda,
+                                  const uint8_t* B, int64_t stride_be, int64_t stride_bn,
+                                  const void* scales, int64_t stride_se, int64_t stride_sn,
+                                  const int32_t* expert_ids, const int32_t* row_pairs, int G,
+                                  int max_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                                  void* stream) {
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk || G < 0 || max_m < 1 || max_m > 16) return -1;
+  if (!a || !B || !scales || !expert_ids || !row_pairs || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  if (G == 0) return 0;
+  FwdArgs p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.row_off = row_pairs;
+  p.ro_shift = 1;
+  p.G = G;
+  p.max_m = max_m;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, max_m, s) : launch_fwd<kMX>(p, max_m, s);
 }
 
 int gnf4_hip_grouped_fwd_tiles(int fmt, const void* a, int a_dtype, int64_t lda, const uint8_t* B,

@@ -405,6 +405,22 @@ def _np_ids(ids):
     return np.asarray([int(e) for e in ids], dtype=np.int32)
 
 
+def _largest_first(expert_ids, sizes_i):
+    """A decode launch's groups in dispatch order, largest first (stable):
+    int32 numpy expert ids [G] and (first row, end row) pairs [2 G] for
+    ``gnf4_hip_grouped_decode_pairs``. Each output row is computed on its
+    own, so the order changes no bits; it starts the workgroups of the
+    groups with the most rows first."""
+    sz = np.asarray(sizes_i, dtype=np.int32)
+    first = np.zeros(len(sz), dtype=np.int32)
+    np.cumsum(sz[:-1], out=first[1:])
+    order = np.argsort(-sz, kind="stable")
+    pairs = np.empty((len(sz), 2), dtype=np.int32)
+    pairs[:, 0] = first[order]
+    pairs[:, 1] = first[order] + sz[order]
+    return _np_ids(expert_ids)[order], pairs.reshape(-1)
+
+
 def _tiles_np(sizes_i, block_m: int):
     """``_tiles_host`` as int32 numpy arrays (same tiles, same order), for
     the launch paths: the host planning of a call stays a few numpy ops."""
@@ -683,6 +699,7 @@ class GroupPlan:
         self.eids = torch.tensor(ids, dtype=torch.int32, device=self.device)
         self.host_ids = np.asarray([int(e) for e in ids], dtype=np.int32)
         self.host_row_off = None
+        self.eids_lf = self.row_pairs = None
         self._tables = {}
         if self.decode:
             row_off = [0]
@@ -691,6 +708,11 @@ class GroupPlan:
             self.row_off = torch.tensor(row_off, dtype=torch.int32, device=self.device)
             if not self.one_row_each:
                 self.host_row_off = np.asarray(row_off, dtype=np.int32)
+                # the launches that leave the GEMV classes take the groups
+                # largest first (gnf4_hip_grouped_decode_pairs)
+                ids_lf, pairs = _largest_first(self.host_ids, sizes_i)
+                self.eids_lf = torch.from_numpy(ids_lf).to(self.device)
+                self.row_pairs = torch.from_numpy(pairs).to(self.device)
         else:
             self.row_off = None
             if shape is not None:
@@ -740,6 +762,15 @@ def launch_planned(fmt: int, a_cat, W, S, plan: GroupPlan, out=None):
         if rc != 1:
             _hiplib.check(rc, "launch_planned")
             return out
+    if plan.decode and plan.G > 0 and plan.row_pairs is not None:
+        with torch.cuda.device(dev):
+            rc = lib.gnf4_hip_grouped_decode_pairs(
+                fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+                plan.eids_lf.data_ptr(), plan.row_pairs.data_ptr(), plan.G, plan.max_m,
+                N, K, out.data_ptr(), out.stride(0), _stream_ptr(dev))
+        _hiplib.check(rc, "launch_planned")
+        return out
     with torch.cuda.device(dev):
         rc = lib.gnf4_hip_grouped_fwd(
             fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
@@ -793,6 +824,19 @@ def _launch_fwd(fmt: int, a_cat, W, S, sizes, expert_ids, block_m, op, fp32w=Fal
             # one row per group: group g is row g, no offset table to upload
             (e_p,), keep = _upload_tables((host_eids,), dev, stream, host_ok=True)
             r_ptr = None
+        elif eids_dev is None:
+            # host ids: the groups largest first, as (first, end) row pairs
+            ids_lf, pairs = _largest_first(expert_ids, sizes_i)
+            (e_p, p_p), keep = _upload_tables((ids_lf, pairs), dev, stream, host_ok=True)
+            with _device_ctx(dev):
+                rc = lib.gnf4_hip_grouped_decode_pairs(
+                    fmt, a_cat.data_ptr(), _hiplib.DTYPE_BF16, a_cat.stride(0),
+                    W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0),
+                    S.stride(1), e_p, p_p, G, max_m, N, K, out.data_ptr(), out.stride(0),
+                    stream.cuda_stream)
+            del keep
+            _hiplib.check(rc, op)
+            return out
         else:
             row_off = [0]
             for m in sizes_i:

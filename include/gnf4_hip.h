@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 12
+#define GNF4_HIP_ABI_VERSION 13
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -132,6 +132,25 @@ int gnf4_hip_grouped_decode_ids(int fmt, const void *a, int a_dtype, int64_t lda
                                 const int32_t *expert_ids, const int32_t *row_off, int G,
                                 int max_m, int64_t N, int64_t K, void *out, int64_t ldo,
                                 void *stream);
+
+/* Grouped decode forward (every group at most max_m <= 16 rows) whose row
+ * table is a (first row, end row) pair per group, row_pairs[2 G] in device
+ * memory (or pinned host memory at its device address), next to
+ * expert_ids[G]: group g covers rows [row_pairs[2 g], row_pairs[2 g + 1]).
+ * The groups need not come in row order, so a caller can list them largest
+ * first, and the workgroups of the groups with the most rows are
+ * dispatched first. Same kernels and bits per row as gnf4_hip_grouped_fwd's
+ * decode path. Returns -1 on bad arguments (as gnf4_hip_grouped_fwd). No
+ * counterpart in the reference; it replaces the decode launches of
+ * gemm_4bit_grouped / gemm_mxfp4_grouped (reference
+ * kernel/nf4_grouped.py:750-806, kernel/mxfp4_grouped.py:146-160) for
+ * callers that hold the group sizes on the host. */
+int gnf4_hip_grouped_decode_pairs(int fmt, const void *a, int a_dtype, int64_t lda,
+                                  const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                                  const void *scales, int64_t stride_se, int64_t stride_sn,
+                                  const int32_t *expert_ids, const int32_t *row_pairs, int G,
+                                  int max_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                                  void *stream);
 
 /* Grouped forward on 256-row tiles with the tile table in host memory: the
  * table (at most 256 m-tiles) travels in the kernel's arguments, so the call

@@ -200,3 +200,83 @@ def test_kernel_argument_expert_ids_planned_and_many_groups(monkeypatch):
     for g in (0, 7, 399):
         one = op(a[g:g + 1], W, S, [1], [ids[g]])
         assert torch.equal(got[g].view(torch.int16), one[0].view(torch.int16)), g
+
+
+# ---------------------------------------------- (first, end) row-pair tables --
+
+def _pairs_call(fmt, a, W, S, ids_dev, pairs_dev, G, max_m, out):
+    import _hiplib
+    W, S = nf4_grouped._aligned_rows(W, 16), nf4_grouped._scales_view(S)
+    rc = _hiplib.load().gnf4_hip_grouped_decode_pairs(
+        0 if fmt == "nf4" else 1, a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
+        W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
+        ids_dev.data_ptr(), pairs_dev.data_ptr(), G, max_m, W.shape[1], a.shape[1],
+        out.data_ptr(), out.stride(0), torch.cuda.current_stream().cuda_stream)
+    _hiplib.check(rc, "decode_pairs")
+
+
+@pytest.mark.parametrize("fmt,N,K,hi", [("nf4", 2048, 768, 3), ("nf4", 1536, 2048, 9),
+                                        ("nf4", 256, 512, 16), ("mxfp4", 640, 1440, 5),
+                                        ("mxfp4", 256, 2880, 1)])
+def test_row_pairs_in_any_order_give_the_prefix_table_bits(fmt, N, K, hi):
+    """Groups listed in a random order as (first, end) row pairs: every row
+    is the bits of the prefix-offset launch of the same groups (the device
+    id form, which keeps the groups in row order). Empty groups included."""
+    op, stack = _ops()[fmt]
+    E, G = 20, 37
+    W, S = stack(E, N, K, seed=40)
+    g = torch.Generator().manual_seed(41)
+    sizes = torch.randint(0, hi + 1, (G,), generator=g).tolist()
+    sizes[0], sizes[5] = hi, 0
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    T = sum(sizes)
+    a = rand_acts(T, K, seed=42)
+    want = op(a, W, S, sizes, torch.tensor(ids, device="cuda"))
+    first = [sum(sizes[:i]) for i in range(G)]
+    perm = torch.randperm(G, generator=g).tolist()
+    pairs = [v for i in perm for v in (first[i], first[i] + sizes[i])]
+    out = torch.full((T, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    _pairs_call(fmt, a, W, S, torch.tensor([ids[i] for i in perm], dtype=torch.int32,
+                                           device="cuda"),
+                torch.tensor(pairs, dtype=torch.int32, device="cuda"), G, max(sizes), out)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    # the op with host ids (largest first) and the planned launch agree
+    got = op(a, W, S, sizes, ids)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    plan = nf4_grouped.GroupPlan(sizes, ids, "cuda")
+    assert plan.row_pairs is not None
+    planned = nf4_grouped.launch_planned(0 if fmt == "nf4" else 1, a, W, S, plan)
+    assert torch.equal(planned.view(torch.int16), want.view(torch.int16))
+
+
+def test_row_pairs_past_65535_groups():
+    """70000 groups of one or two rows as row pairs, largest first: the
+    launch runs as several grid ranges (each taking its slice of the pair
+    table); the bits are those of the prefix-offset launch."""
+    op, stack = _ops()["nf4"]
+    E, N, K, G = 4, 32, 128, 70000
+    W, S = stack(E, N, K, seed=43)
+    g = torch.Generator().manual_seed(44)
+    sizes = (1 + (torch.rand(G, generator=g) < 0.1).int()).tolist()
+    ids = torch.randint(0, E, (G,), generator=g).tolist()
+    a = rand_acts(sum(sizes), K, seed=45)
+    want = op(a, W, S, sizes, torch.tensor(ids, device="cuda"))
+    got = op(a, W, S, sizes, ids)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_row_pair_tables_reject_bad_arguments():
+    import _hiplib
+    lib = _hiplib.load()
+    W, S = rand_nf4_stack(2, 64, 128, seed=46)
+    a = rand_acts(4, 128, seed=47)
+    out = torch.empty(4, 64, dtype=torch.bfloat16, device="cuda")
+    ids = torch.zeros(2, dtype=torch.int32, device="cuda")
+    pairs = torch.tensor([0, 2, 2, 4], dtype=torch.int32, device="cuda")
+    for max_m, p in ((0, pairs), (17, pairs), (2, None)):
+        rc = lib.gnf4_hip_grouped_decode_pairs(
+            0, a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0), W.data_ptr(), W.stride(0),
+            W.stride(1), S.data_ptr(), S.stride(0), S.stride(1), ids.data_ptr(),
+            p.data_ptr() if p is not None else None, 2, max_m, 64, 128, out.data_ptr(),
+            out.stride(0), torch.cuda.current_stream().cuda_stream)
+        assert rc == -1

@@ -333,6 +333,9 @@ struct FwdArgs {
   // host only: group ids and row offsets to pass in the GEMV kernels'
   // arguments (GemvIds), or null (the kernels read eids / row_off)
   const struct GemvIds* ids_inline;
+  // host only: the groups come from device routing and any of them may be
+  // empty (the launch covers a bound of the active groups)
+  int sparse_groups;
 };
 
 // The groups of a decode launch of at most kGemvIdsMax groups, in the GEMV
@@ -4082,7 +4085,12 @@ int launch_stream_inst(const FwdArgs& p, dim3 grid, int upg, int per_wg, int lds
 template <int FMT>
 int launch_stream(const FwdArgs& p, hipStream_t stream) {
   if constexpr (FMT != kMX) {
-    // NF4: k_decode_stream_nf4, 16-row units, one unit in flight per team
+    // NF4: k_decode_stream_nf4, 16-row units, one unit in flight per team.
+    // Its workgroups are dealt to the groups in equal shares, so where groups
+    // may be empty (device routing: the launch covers a bound of the active
+    // groups) their shares would idle: the per-unit kernel spreads the units
+    // instead (Qwen3 batch 16 routed FFN: 81.3 -> 74.8 us)
+    if (p.sparse_groups) return 1;
     if (p.max_m < 2 || p.max_m > 8 || p.row_off == nullptr || p.G <= 0 || p.G > 65535) return 1;
     const int64_t nchunks = (p.K + 127) / 128;
     if (decode_cpw<FMT>(p.K, p.max_m) != 2 || nchunks > 16) return 1;   // 1024 < K <= 2048
@@ -4120,6 +4128,7 @@ int launch_stream(const FwdArgs& p, hipStream_t stream) {
                        (int)upg, (int)per_wg);
     return hipGetLastError() == hipSuccess ? 0 : -2;
   } else {
+    if (p.sparse_groups) return 1;
     if (p.max_m < 2 || p.max_m > 16 || p.row_off == nullptr || p.G <= 0 || p.G > 65535) return 1;
     const int64_t nchunks = (p.K + 127) / 128;
     if (decode_cpw<FMT>(p.K, p.max_m) != 3 || nchunks > 8 * 3) return 1;
@@ -5021,6 +5030,42 @@ int gnf4_hip_grouped_decode_pairs(int fmt, const void* a, int a_dtype, int64_t l
   p.K = K;
   p.out = static_cast<uint16_t*>(out);
   p.ldo = ldo;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, max_m, s) : launch_fwd<kMX>(p, max_m, s);
+}
+
+int gnf4_hip_grouped_decode_routed(int fmt, const void* a, int a_dtype, int64_t lda,
+                                   const uint8_t* B, int64_t stride_be, int64_t stride_bn,
+                                   const void* scales, int64_t stride_se, int64_t stride_sn,
+                                   const int32_t* expert_ids, const int32_t* row_off, int G,
+                                   int max_m, int64_t N, int64_t K, void* out, int64_t ldo,
+                                   void* stream) {
+  const int64_t blk = fmt == GNF4_FMT_NF4 ? 64 : 32;
+  if ((fmt != GNF4_FMT_NF4 && fmt != GNF4_FMT_MXFP4) || a_dtype != GNF4_DTYPE_BF16) return -1;
+  if (N <= 0 || K <= 0 || K % blk || G < 0 || max_m < 1 || max_m > 16) return -1;
+  if (!a || !B || !scales || !expert_ids || !row_off || !out) return -1;
+  if (lda < K || lda % 8 || ldo < N || stride_bn % 16 || stride_be % 16 || !aligned16(B) ||
+      !aligned16(a))
+    return -1;
+  if (G == 0) return 0;
+  FwdArgs p{};
+  p.a = static_cast<const uint16_t*>(a);
+  p.lda = lda;
+  p.B = B;
+  p.sbe = stride_be;
+  p.sbn = stride_bn;
+  p.S = scales;
+  p.sse = stride_se;
+  p.ssn = stride_sn;
+  p.eids = expert_ids;
+  p.row_off = row_off;
+  p.G = G;
+  p.max_m = max_m;
+  p.N = N;
+  p.K = K;
+  p.out = static_cast<uint16_t*>(out);
+  p.ldo = ldo;
+  p.sparse_groups = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return fmt == GNF4_FMT_NF4 ? launch_fwd<kNF4>(p, max_m, s) : launch_fwd<kMX>(p, max_m, s);
 }

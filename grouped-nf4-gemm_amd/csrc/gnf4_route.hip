@@ -197,9 +197,17 @@ __global__ void __launch_bounds__(256) k_route_topk(const float* __restrict__ lo
 // as many as out-of-range ids); pos[i] = grouped position of row i (-1 for
 // an out-of-range expert id, which is also flagged in info[2]); info[0] =
 // active groups, info[1] = the largest group.
+// cap > 0: an expert's rows form groups of at most cap rows (consecutive
+// groups, the same expert id), so no group is larger than cap.
 // `order_lds`, when not null, receives a copy of `order` in LDS.
+// Groups of an expert with c rows: 0, 1, or ceil(c / cap) when capped.
+__device__ __forceinline__ int groups_of(int c, int cap) {
+  return c <= 0 ? 0 : cap > 0 ? (c + cap - 1) / cap : 1;
+}
+
 __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_stride, int64_t T,
-                                           int k, int E, int slots, int32_t* __restrict__ eids,
+                                           int k, int E, int slots, int cap,
+                                           int32_t* __restrict__ eids,
                                            int32_t* __restrict__ row_off,
                                            int32_t* __restrict__ order,
                                            int32_t* __restrict__ pos,
@@ -241,7 +249,7 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
   }
   // (3) inclusive scans of totals and of the active flag over experts
   s_scan[tid] = tid < E ? tot : 0;
-  s_scan2[tid] = tid < E && tot > 0 ? 1 : 0;
+  s_scan2[tid] = tid < E ? groups_of(tot, cap) : 0;
   __syncthreads();
   for (int off = 1; off < kGroupThreads; off <<= 1) {
     const int a = tid >= off ? s_scan[tid - off] : 0;
@@ -255,12 +263,13 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     const int base = s_scan[tid] - tot;
     s_base[tid] = base;
     if (tot > 0) {
-      const int g = s_scan2[tid] - 1;
-      if (g < slots) {
-        eids[g] = tid;
-        row_off[g] = base;
+      const int ng = groups_of(tot, cap);
+      const int g = s_scan2[tid] - ng;
+      for (int j = 0; j < ng && g + j < slots; ++j) {
+        eids[g + j] = tid;
+        row_off[g + j] = base + j * cap;
       }
-      atomicMax(&s_max, tot);
+      atomicMax(&s_max, cap > 0 && tot > cap ? cap : tot);
     }
   }
   const int active = s_scan2[kGroupThreads - 1];
@@ -309,9 +318,9 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
 
 __global__ void __launch_bounds__(kGroupThreads) k_route_groups(
     const int64_t* __restrict__ ids, int64_t ids_stride, int64_t T, int k, int E, int slots,
-    int32_t* __restrict__ eids, int32_t* __restrict__ row_off, int32_t* __restrict__ order,
-    int32_t* __restrict__ pos, int32_t* __restrict__ info) {
-  group_rows(ids, ids_stride, T, k, E, slots, eids, row_off, order, pos, info);
+    int cap, int32_t* __restrict__ eids, int32_t* __restrict__ row_off,
+    int32_t* __restrict__ order, int32_t* __restrict__ pos, int32_t* __restrict__ info) {
+  group_rows(ids, ids_stride, T, k, E, slots, cap, eids, row_off, order, pos, info);
 }
 
 // group_rows' outputs computed by one wave (the calling wave, all 64 lanes)
@@ -322,7 +331,7 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_groups(
 // i after the earlier rows of its expert. Same outputs, bit for bit. `ids`
 // is the row-major [T, k] array (row i at ids[i]).
 __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, int k, int E,
-                                                int slots, int32_t* __restrict__ eids,
+                                                int slots, int cap, int32_t* __restrict__ eids,
                                                 int32_t* __restrict__ row_off,
                                                 int32_t* __restrict__ order,
                                                 int32_t* __restrict__ pos,
@@ -352,8 +361,9 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
     const int e = lane * P + j;
     c[j] = j < P && e < E ? s_cnt[e] : 0;
     tot += c[j];
-    act += c[j] > 0;
-    mx = c[j] > mx ? c[j] : mx;
+    act += groups_of(c[j], cap);
+    const int cm = cap > 0 && c[j] > cap ? cap : c[j];
+    mx = cm > mx ? cm : mx;
   }
   int tot_x = tot, act_x = act;   // inclusive scans over lanes
 #pragma unroll
@@ -370,12 +380,12 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
     const int e = lane * P + j;
     if (j < P && e < E) {
       s_base[e] = base;
-      if (c[j] > 0) {
+      const int ng = groups_of(c[j], cap);
+      for (int t = 0; t < ng; ++t, ++g) {
         if (g < slots) {
           eids[g] = e;
-          row_off[g] = base;
+          row_off[g] = base + t * cap;
         }
-        ++g;
       }
       base += c[j];
     }
@@ -431,7 +441,7 @@ template <int kPerLane>
 __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     const float* __restrict__ logits, int64_t ld, int64_t T, int E, int k, int mode, int norm,
     int64_t* idx, int64_t idx_stride, uint16_t* __restrict__ wts, int64_t wts_stride,
-    const uint16_t* __restrict__ x, int64_t ldx, int64_t K, int slots,
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t K, int slots, int cap,
     int32_t* __restrict__ eids, int32_t* __restrict__ row_off, int32_t* __restrict__ order,
     int32_t* __restrict__ pos, int32_t* __restrict__ info, uint16_t* __restrict__ a_out,
     int64_t lda) {
@@ -458,10 +468,10 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
   // the grouping: by one wave, with no workgroup barriers, for up to 64 rows
   if (N <= 64) {
     if (wave == 0)
-      group_rows_wave(s_ids, T, k, E, slots, eids, row_off, order, pos, info, s_order, s_cnt1,
-                      s_base1);
+      group_rows_wave(s_ids, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order,
+                      s_cnt1, s_base1);
   } else {
-    group_rows(s_ids, k, T, k, E, slots, eids, row_off, order, pos, info, s_order);
+    group_rows(s_ids, k, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order);
   }
   __syncthreads();
   // 32-bit index math (the host checks T * k * K < 2^31)
@@ -604,24 +614,25 @@ int gnf4_hip_route_topk(const float* logits, int64_t T, int64_t E, int64_t ld, i
 }
 
 int gnf4_hip_route_groups(const int64_t* topk_ids, int64_t ids_stride, int64_t T, int k,
-                          int64_t E, int slots, int32_t* eids, int32_t* row_off, int32_t* order,
-                          int32_t* pos, int32_t* info, void* stream) {
-  if (T < 0 || k < 1 || ids_stride < k || E <= 0 || E > kGroupMaxE || slots < 0) return -1;
+                          int64_t E, int slots, int cap, int32_t* eids, int32_t* row_off,
+                          int32_t* order, int32_t* pos, int32_t* info, void* stream) {
+  if (T < 0 || k < 1 || ids_stride < k || E <= 0 || E > kGroupMaxE || slots < 0 || cap < 0)
+    return -1;
   if (T * k > 0x7FFFFFFF) return -1;
   if (!topk_ids || !eids || !row_off || !order || !pos || !info) return -1;
   hipLaunchKernelGGL(k_route_groups, dim3(1), dim3(kGroupThreads), 0,
                      static_cast<hipStream_t>(stream), topk_ids, ids_stride, T, k, (int)E,
-                     slots, eids, row_off, order, pos, info);
+                     slots, cap, eids, row_off, order, pos, info);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 int gnf4_hip_route_decode(const float* logits, int64_t ld, int64_t T, int64_t E, int k,
                           int mode, int norm, int64_t* idx, int64_t idx_stride, uint16_t* wts,
                           int64_t wts_stride, const void* x, int64_t ldx, int64_t K, int slots,
-                          int32_t* eids, int32_t* row_off, int32_t* order, int32_t* pos,
+                          int cap, int32_t* eids, int32_t* row_off, int32_t* order, int32_t* pos,
                           int32_t* info, void* a_out, int64_t lda, void* stream) {
   if (T < 0 || T > kGroupWaves || E <= 0 || E > kGroupMaxE || k < 1 || k > kRouteMaxK ||
-      k > E || idx_stride < k || slots < 0 || K <= 0 || K % 8 || ldx < K || ldx % 8 ||
+      k > E || idx_stride < k || slots < 0 || cap < 0 || K <= 0 || K % 8 || ldx < K || ldx % 8 ||
       lda < K || lda % 8)
     return -1;
   if (logits && (ld < E || (mode != 0 && mode != 1) || !wts || wts_stride < k)) return -1;
@@ -634,8 +645,8 @@ int gnf4_hip_route_decode(const float* logits, int64_t ld, int64_t T, int64_t E,
 #define GNF4_PRO(P)                                                                           \
   hipLaunchKernelGGL((k_route_decode<P>), dim3(1), dim3(kGroupThreads), 0, s, logits, ld, T,   \
                      (int)E, k, mode, norm, idx, idx_stride, wts, wts_stride,                  \
-                     static_cast<const uint16_t*>(x), ldx, K, slots, eids, row_off, order, pos, \
-                     info, static_cast<uint16_t*>(a_out), lda)
+                     static_cast<const uint16_t*>(x), ldx, K, slots, cap, eids, row_off, order, \
+                     pos, info, static_cast<uint16_t*>(a_out), lda)
   if (per_lane <= 1)
     GNF4_PRO(1);
   else if (per_lane <= 2)

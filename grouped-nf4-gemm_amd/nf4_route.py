@@ -35,6 +35,18 @@ from nf4_grouped import DECODE_MAX_ROWS, _aligned_rows, _require_gpu, _scales_vi
 
 ROUTE_MAX_K = 64          # as the reference's epilogue
 ROUTE_MAX_EXPERTS = 512   # grouping kernel's LDS tables
+# Largest group of the device-routed decode path: an expert's rows beyond it
+# form further groups, so the expert FFN launches in the class of at most 8
+# rows (the split-table kernels' one row set) instead of T rows (two row
+# sets at T > 8; Qwen3 batch 16: 123 us -> about the host-routed 67 us)
+DECODE_GROUP_CAP = 8
+
+
+def route_slots(N: int, E: int, cap: int = 0) -> int:
+    """Group-table size that holds every routing of N rows over E experts
+    with groups of at most ``cap`` rows (0: one group per expert)."""
+    M = min(N, E)
+    return max(1, M + ((N - M) // cap if cap > 0 else 0))
 
 
 def _dev_check(t, op):
@@ -75,7 +87,8 @@ class RoutePlan:
     """Device tables of one routing: ``eids [slots]``, ``row_off [slots + 1]``
     (groups past the active count are empty), ``order [N]`` (grouped
     position -> routed row t * k + j), ``pos [N]`` (its inverse) and
-    ``info [3]`` (active groups, largest group, bad-id flag)."""
+    ``info [3]`` (active groups, largest group, bad-id flag). ``cap``: the
+    largest group the grouping allowed (0: one group per expert)."""
     eids: torch.Tensor
     row_off: torch.Tensor
     order: torch.Tensor
@@ -85,6 +98,7 @@ class RoutePlan:
     k: int
     E: int
     slots: int
+    cap: int = 0
 
     @property
     def rows(self) -> int:
@@ -93,8 +107,10 @@ class RoutePlan:
     def max_rows_bound(self) -> int:
         """An upper bound of the largest group known without a device read:
         an expert appears at most once per token when the top-k ids of a
-        token are distinct (as the selection guarantees)."""
-        return min(self.T, self.rows)
+        token are distinct (as the selection guarantees), and no group
+        exceeds the grouping's cap."""
+        b = min(self.T, self.rows)
+        return min(b, self.cap) if self.cap > 0 else b
 
     def host_groups(self):
         """(sizes, expert_ids) of the active groups as host lists. Reads the
@@ -108,8 +124,10 @@ class RoutePlan:
         return bool(self.info[2].item())
 
 
-def route_groups(topk_ids: torch.Tensor, n_experts: int, slots: int | None = None) -> RoutePlan:
-    """Group the T * k routed rows by expert on the device (one launch)."""
+def route_groups(topk_ids: torch.Tensor, n_experts: int, slots: int | None = None,
+                 cap: int = 0) -> RoutePlan:
+    """Group the T * k routed rows by expert on the device (one launch);
+    ``cap`` > 0 splits an expert's rows into groups of at most cap rows."""
     _dev_check(topk_ids, "route_groups")
     if topk_ids.dim() != 2:
         raise ValueError(f"topk_ids must be [T, k], got {tuple(topk_ids.shape)}")
@@ -120,8 +138,10 @@ def route_groups(topk_ids: torch.Tensor, n_experts: int, slots: int | None = Non
         ids = ids.contiguous()
     T, k = ids.shape
     N = T * k
+    if cap < 0:
+        raise ValueError(f"cap={cap} must be >= 0")
     if slots is None:
-        slots = max(1, min(N, n_experts))
+        slots = route_slots(N, n_experts, cap)
     dev = ids.device
     eids = torch.empty(slots, dtype=torch.int32, device=dev)
     row_off = torch.empty(slots + 1, dtype=torch.int32, device=dev)
@@ -130,11 +150,11 @@ def route_groups(topk_ids: torch.Tensor, n_experts: int, slots: int | None = Non
     info = torch.empty(3, dtype=torch.int32, device=dev)
     with torch.cuda.device(dev):
         rc = _hiplib.load().gnf4_hip_route_groups(
-            ids.data_ptr(), ids.stride(0), T, k, n_experts, slots, eids.data_ptr(),
+            ids.data_ptr(), ids.stride(0), T, k, n_experts, slots, cap, eids.data_ptr(),
             row_off.data_ptr(), order.data_ptr(), pos.data_ptr(), info.data_ptr(),
             _stream_ptr(dev))
     _hiplib.check(rc, "route_groups")
-    return RoutePlan(eids, row_off, order, pos, info, T, k, n_experts, slots)
+    return RoutePlan(eids, row_off, order, pos, info, T, k, n_experts, slots, cap)
 
 
 def gather_rows(x: torch.Tensor, plan: RoutePlan) -> torch.Tensor:
@@ -189,22 +209,24 @@ def _decode_fwd(a, W, S, plan: RoutePlan, max_m: int):
     W, S = _aligned_rows(W, 16), _scales_view(S)
     out = torch.empty(a.shape[0], N, dtype=torch.bfloat16, device=a.device)
     with torch.cuda.device(a.device):
-        rc = _hiplib.load().gnf4_hip_grouped_fwd(
+        rc = _hiplib.load().gnf4_hip_grouped_decode_routed(
             _hiplib.FMT_NF4, a.data_ptr(), _hiplib.DTYPE_BF16, a.stride(0),
             W.data_ptr(), W.stride(0), W.stride(1), S.data_ptr(), S.stride(0), S.stride(1),
-            plan.eids.data_ptr(), plan.row_off.data_ptr(), plan.slots, None, None, None, 0,
-            max_m, N, K, out.data_ptr(), out.stride(0), _stream_ptr(a.device))
+            plan.eids.data_ptr(), plan.row_off.data_ptr(), plan.slots, max_m, N, K,
+            out.data_ptr(), out.stride(0), _stream_ptr(a.device))
     _hiplib.check(rc, "moe_ffn")
     return out
 
 
-def _route_decode(x, n_experts, k, topk_ids=None, logits=None, mode=0, norm=False):
+def _route_decode(x, n_experts, k, topk_ids=None, logits=None, mode=0, norm=False,
+                  cap=DECODE_GROUP_CAP):
     """The one-launch decode prologue (T <= 16): top-k (when ``logits`` is
-    given), grouping and gather. Returns (plan, gathered rows, ids, weights)."""
+    given), grouping (groups of at most ``cap`` rows) and gather. Returns
+    (plan, gathered rows, ids, weights)."""
     T, K = x.shape
     dev = x.device
     N = T * k
-    slots = max(1, min(N, n_experts))
+    slots = route_slots(N, n_experts, cap)
     if logits is not None:
         lg = logits.float()
         if lg.stride(-1) != 1:
@@ -222,12 +244,12 @@ def _route_decode(x, n_experts, k, topk_ids=None, logits=None, mode=0, norm=Fals
                      torch.empty(slots + 1, dtype=torch.int32, device=dev),
                      torch.empty(max(N, 1), dtype=torch.int32, device=dev),
                      torch.empty(max(N, 1), dtype=torch.int32, device=dev),
-                     torch.empty(3, dtype=torch.int32, device=dev), T, k, n_experts, slots)
+                     torch.empty(3, dtype=torch.int32, device=dev), T, k, n_experts, slots, cap)
     a = torch.empty(N, K, dtype=torch.bfloat16, device=dev)
     with torch.cuda.device(dev):
         rc = _hiplib.load().gnf4_hip_route_decode(
             lg_ptr, ld, T, n_experts, k, mode, int(bool(norm)), ids.data_ptr(), ids.stride(0),
-            w_ptr, k, x.data_ptr(), x.stride(0), K, slots, plan.eids.data_ptr(),
+            w_ptr, k, x.data_ptr(), x.stride(0), K, slots, cap, plan.eids.data_ptr(),
             plan.row_off.data_ptr(), plan.order.data_ptr(), plan.pos.data_ptr(),
             plan.info.data_ptr(), a.data_ptr(), a.stride(0), _stream_ptr(dev))
     _hiplib.check(rc, "route_decode")

@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define GNF4_HIP_ABI_VERSION 13
+#define GNF4_HIP_ABI_VERSION 14
 
 #define GNF4_FMT_NF4 0
 #define GNF4_FMT_MXFP4 1
@@ -151,6 +151,20 @@ int gnf4_hip_grouped_decode_pairs(int fmt, const void *a, int a_dtype, int64_t l
                                   const int32_t *expert_ids, const int32_t *row_pairs, int G,
                                   int max_m, int64_t N, int64_t K, void *out, int64_t ldo,
                                   void *stream);
+
+/* Grouped decode forward over device-routing tables (gnf4_hip_route_groups
+ * / gnf4_hip_route_decode: eids [G], row_off [G + 1], G = their slots, max_m
+ * a bound of the largest group), where any group may be empty: the same
+ * kernels and bits as gnf4_hip_grouped_fwd's decode path, minus the unit
+ * walk that deals its workgroups to the groups in equal shares (the shares
+ * of empty groups would idle). -1 on bad arguments. No counterpart in the
+ * reference (its routing is on the host, kernel/arena_moe_patch.py:41-66). */
+int gnf4_hip_grouped_decode_routed(int fmt, const void *a, int a_dtype, int64_t lda,
+                                   const uint8_t *B, int64_t stride_be, int64_t stride_bn,
+                                   const void *scales, int64_t stride_se, int64_t stride_sn,
+                                   const int32_t *expert_ids, const int32_t *row_off, int G,
+                                   int max_m, int64_t N, int64_t K, void *out, int64_t ldo,
+                                   void *stream);
 
 /* Grouped forward on 256-row tiles with the tile table in host memory: the
  * table (at most 256 m-tiles) travels in the kernel's arguments, so the call
@@ -398,21 +412,27 @@ int gnf4_hip_route_topk(const float *logits, int64_t T, int64_t E, int64_t ld, i
  * the active count are empty), order [N] int32 (grouped position -> row),
  * pos [N] int32 (row -> grouped position, -1 for an id outside [0, E)),
  * info [3] int32 (active groups, largest group, 1 if an id was out of
- * range). E <= 512. slots = min(N, E) holds every case; the tables can be
- * passed straight to the decode forward / fused FFN with G = slots. */
+ * range). E <= 512. cap > 0 splits an expert's rows into consecutive
+ * groups of at most cap rows (same expert id; cap = 0: one group per
+ * expert), so the largest group is at most cap rows and a decode launch
+ * can take the class of cap rows instead of T. With M = min(N, E), slots =
+ * M + (N - M) / cap (slots = M when cap = 0) holds every case; the tables
+ * can be passed straight to the decode forward / fused FFN with G = slots.
+ * (The reference's dispatch has one group per expert; the split groups
+ * give every row the bits of the same rows in one group of that class.) */
 int gnf4_hip_route_groups(const int64_t *topk_ids, int64_t ids_stride, int64_t T, int k,
-                          int64_t E, int slots, int32_t *eids, int32_t *row_off,
+                          int64_t E, int slots, int cap, int32_t *eids, int32_t *row_off,
                           int32_t *order, int32_t *pos, int32_t *info, void *stream);
 
 /* The decode routing prologue in one launch (T <= 16 tokens, E <= 512):
  * gnf4_hip_route_topk (skipped when logits is NULL: idx then holds the
  * caller's ids), gnf4_hip_route_groups and gnf4_hip_gather_rows, with the
- * same arguments and outputs; a_out [T * k, lda] receives the gathered
- * rows of x [T, ldx]. */
+ * same arguments and outputs (cap as for gnf4_hip_route_groups); a_out
+ * [T * k, lda] receives the gathered rows of x [T, ldx]. */
 int gnf4_hip_route_decode(const float *logits, int64_t ld, int64_t T, int64_t E, int k,
                           int mode, int norm, int64_t *idx, int64_t idx_stride,
                           uint16_t *wts, int64_t wts_stride, const void *x, int64_t ldx,
-                          int64_t K, int slots, int32_t *eids, int32_t *row_off,
+                          int64_t K, int slots, int cap, int32_t *eids, int32_t *row_off,
                           int32_t *order, int32_t *pos, int32_t *info, void *a_out,
                           int64_t lda, void *stream);
 

@@ -134,12 +134,26 @@ def _qwen_stack(seed):
     return gu_p, gu_a, dn_p, dn_a
 
 
-def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused, class_rows=None):
+def _split(sizes, eids, cap):
+    """Groups of at most cap rows: an expert's rows as consecutive groups."""
+    s2, e2 = [], []
+    for m, e in zip(sizes, eids):
+        while m > cap:
+            s2.append(cap)
+            e2.append(e)
+            m -= cap
+        s2.append(m)
+        e2.append(e)
+    return s2, e2
+
+
+def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused, class_rows=None, cap=None):
     """The reference's MoE block arithmetic with host routing: stable sort by
     expert, the grouped FFN op on the sorted rows, weighted sum over slots.
     ``class_rows``: run the grouped op in the launch class of that largest
     group (one extra group of that many zero rows, whose outputs are
-    dropped), as the device-routed path does with its bound min(T, 16)."""
+    dropped), as the device-routed path does with its bound min(T, cap).
+    ``cap``: an expert's rows as groups of at most cap rows."""
     import nf4_ffn
     T, k = ids.shape
     flat = ids.reshape(-1).cpu()
@@ -147,6 +161,8 @@ def _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused, class_rows=None):
     counts = torch.bincount(flat, minlength=QWEN["E"])
     eids = torch.nonzero(counts).flatten().tolist()
     sizes = counts[counts > 0].tolist()
+    if cap:
+        sizes, eids = _split(sizes, eids, cap)
     a = x[(order // k).cuda()]
     n = a.shape[0]
     if class_rows is not None and class_rows > max(sizes):
@@ -170,9 +186,12 @@ def test_moe_ffn_equals_the_host_routed_composition(T):
     logits = torch.randn(T, QWEN["E"], device="cuda")
     ids, w = r.route_topk(logits, QWEN["k"], 0, True)
     out = r.moe_ffn(x, ids, w, gu_p, gu_a, dn_p, dn_a)
-    # the device path launches in the class of its bound min(T, 16) rows
+    # the device path launches in the class of its bound min(T, 8) rows, its
+    # groups at most 8 rows
+    cap = r.DECODE_GROUP_CAP
     want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None,
-                        class_rows=min(T, 16) if T <= 16 else None)
+                        class_rows=min(T, cap) if T <= 16 else None,
+                        cap=cap if T <= 16 else None)
     assert torch.equal(_bits(out), _bits(want))
     if T <= 16:   # the three-launch decode form over the device tables agrees too
         out3 = r.moe_ffn(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=False)
@@ -250,7 +269,7 @@ def test_one_launch_prologue_equals_the_separate_kernels(T, E, k, mode, norm):
     x = rand_acts(T, 256, seed=T)
     plan, a, ids, wts = r._route_decode(x, E, k, logits=logits, mode=mode, norm=norm)
     ids2, wts2 = r.route_topk(logits, k, mode, bool(norm))
-    plan2 = r.route_groups(ids2, E)
+    plan2 = r.route_groups(ids2, E, cap=r.DECODE_GROUP_CAP)
     assert torch.equal(ids, ids2) and torch.equal(_bits(wts), _bits(wts2))
     for f in ("eids", "row_off", "order", "pos", "info"):
         assert torch.equal(getattr(plan, f), getattr(plan2, f)), f
@@ -289,8 +308,10 @@ def test_moe_layer_from_logits_equals_the_host_routed_composition(T):
     out, ids, w = r.moe_layer(x, logits, QWEN["k"], gu_p, gu_a, dn_p, dn_a, mode=0, norm=True)
     ids2, w2 = r.route_topk(logits, QWEN["k"], 0, True)
     assert torch.equal(ids, ids2) and torch.equal(_bits(w), _bits(w2))
+    cap = r.DECODE_GROUP_CAP
     want = _host_routed(x, ids, w, gu_p, gu_a, dn_p, dn_a, fused=None,
-                        class_rows=min(T, 16) if T <= 16 else None)
+                        class_rows=min(T, cap) if T <= 16 else None,
+                        cap=cap if T <= 16 else None)
     assert torch.equal(_bits(out), _bits(want))
 
 
@@ -319,10 +340,16 @@ def test_one_launch_prologue_grouping_with_caller_ids(T, k, E):
     ids = ids.to("cuda")
     x = rand_acts(T, 256, seed=T + k)
     plan, a, _, _ = r._route_decode(x, E, k, topk_ids=ids)
-    plan2 = r.route_groups(ids, E)
+    plan2 = r.route_groups(ids, E, cap=r.DECODE_GROUP_CAP)
     for f in ("eids", "row_off", "order", "pos", "info"):
         assert torch.equal(getattr(plan, f), getattr(plan2, f)), f
     assert plan.bad_ids()
+    # the capped groups are the uncapped ones cut into runs of at most 8 rows
+    plan0 = r.route_groups(ids, E)
+    assert torch.equal(plan0.order, plan.order) and torch.equal(plan0.pos, plan.pos)
+    s0, e0 = plan0.host_groups()
+    assert plan.host_groups() == _split(s0, e0, r.DECODE_GROUP_CAP)
+    assert int(plan.info[1]) == min(max(s0), r.DECODE_GROUP_CAP)
     # the one row of an out-of-range id has no grouped position: the last
     # position holds -1 and gathers zeros, in both gathers
     assert plan.order.cpu().tolist()[-1] == -1

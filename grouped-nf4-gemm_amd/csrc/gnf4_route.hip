@@ -431,11 +431,15 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
 
 // The whole decode routing prologue in one workgroup (T <= 16 tokens):
 // top-k of each token's logits by one wave (skipped when the caller passes
-// its own ids: logits == nullptr), the grouping, and the gather of the
-// activation rows into group order. The ids and the order stay in LDS
-// between the phases; the gather keeps eight 16-byte loads in flight per
-// thread.
+// its own ids: logits == nullptr), the grouping, and the activation rows in
+// group order. The ids and the order stay in LDS between the phases. Where
+// x fits kDecodeHold 16-byte pieces per thread, it is loaded into registers
+// at the start (its loads overlap the logits' and the top-k), and after the
+// grouping each piece is stored to its token's k grouped positions: no load
+// waits on the grouping. Otherwise the rows are gathered after the grouping,
+// eight 16-byte loads in flight per thread.
 constexpr int kDecodeMaxRows = kGroupWaves * kRouteMaxK;   // T * k <= 1024
+constexpr int kDecodeHold = 8;
 
 template <int kPerLane>
 __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
@@ -447,9 +451,26 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     int64_t lda) {
   __shared__ int64_t s_ids[kDecodeMaxRows];
   __shared__ int32_t s_order[kDecodeMaxRows];
+  __shared__ int32_t s_pos[kDecodeMaxRows];
   __shared__ int32_t s_cnt1[kGroupMaxE], s_base1[kGroupMaxE];
+  __shared__ int32_t s_valid;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int N = (int)(T * k);
+  // 32-bit index math (the host checks T * k * K < 2^31)
+  const int vec = (int)(K / 8);
+  const int xtot = (int)T * vec;
+  const bool hold = xtot <= kDecodeHold * kGroupThreads;   // uniform
+  u32x4_t xv[kDecodeHold];
+  if (hold) {
+#pragma unroll
+    for (int u = 0; u < kDecodeHold; ++u) {
+      const int q = threadIdx.x + u * kGroupThreads;
+      if (q < xtot) {
+        const int t = q / vec, c = (q - t * vec) * 8;
+        xv[u] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)t * ldx + c);
+      }
+    }
+  }
   if (logits) {
     if (wave < T) {
       int sel_i;
@@ -474,8 +495,40 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     group_rows(s_ids, k, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order);
   }
   __syncthreads();
-  // 32-bit index math (the host checks T * k * K < 2^31)
-  const int vec = (int)(K / 8), total = N * vec;
+  if (hold) {
+    // row i's grouped position (-1: an out-of-range id), and the first
+    // position past the valid rows (the positions after it hold -1)
+    if (threadIdx.x == 0) s_valid = N;
+    for (int i = threadIdx.x; i < N; i += kGroupThreads) s_pos[i] = -1;
+    __syncthreads();
+    for (int p = threadIdx.x; p < N; p += kGroupThreads) {
+      const int src = s_order[p];
+      if (src >= 0)
+        s_pos[src] = p;
+      else
+        atomicMin(&s_valid, p);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kDecodeHold; ++u) {
+      const int q = threadIdx.x + u * kGroupThreads;
+      if (q < xtot) {
+        const int t = q / vec, c = (q - t * vec) * 8;
+        for (int j = 0; j < k; ++j) {
+          const int p = s_pos[t * k + j];
+          if (p >= 0) *reinterpret_cast<u32x4_t*>(a_out + (int64_t)p * lda + c) = xv[u];
+        }
+      }
+    }
+    // positions past the valid rows gather nothing: zeros
+    const int v = s_valid;
+    for (int q = v * vec + threadIdx.x; q < N * vec; q += kGroupThreads) {
+      const int r = q / vec, c = (q - r * vec) * 8;
+      *reinterpret_cast<u32x4_t*>(a_out + (int64_t)r * lda + c) = u32x4_t{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+  const int total = N * vec;
   constexpr int kInFlight = 8;
   for (int q0 = threadIdx.x; q0 < total; q0 += kInFlight * kGroupThreads) {
     u32x4_t v[kInFlight];

@@ -355,3 +355,23 @@ def test_one_launch_prologue_grouping_with_caller_ids(T, k, E):
     assert plan.order.cpu().tolist()[-1] == -1
     assert torch.equal(_bits(a), _bits(r.gather_rows(x, plan2)))
     assert torch.count_nonzero(a[-1].float()) == 0
+
+
+@pytest.mark.parametrize("T,K", [(16, 4096), (16, 4104), (3, 256)])
+def test_one_launch_prologue_rows_held_or_gathered(T, K):
+    """The prologue's activation rows: x held in registers from the start
+    and stored to each token's grouped positions (T * K / 8 <= 8 pieces per
+    thread: 16 x 4096 is the edge), or gathered after the grouping (16 x
+    4104): both are gather_rows' bits, zero rows past the valid ones
+    included (one id out of range)."""
+    r = _route()
+    E, k = 128, 8
+    g = torch.Generator().manual_seed(T * 7 + K)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    ids[T - 1, 0] = E + 5
+    ids = ids.to("cuda")
+    x = rand_acts(T, K, seed=K)
+    plan, a, _, _ = r._route_decode(x, E, k, topk_ids=ids)
+    plan2 = r.route_groups(ids, E, cap=r.DECODE_GROUP_CAP)
+    assert torch.equal(_bits(a), _bits(r.gather_rows(x, plan2)))
+    assert torch.count_nonzero(a[-1].float()) == 0

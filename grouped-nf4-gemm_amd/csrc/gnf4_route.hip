@@ -212,7 +212,8 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
                                            int32_t* __restrict__ order,
                                            int32_t* __restrict__ pos,
                                            int32_t* __restrict__ info,
-                                           int32_t* order_lds = nullptr) {
+                                           int32_t* order_lds = nullptr,
+                                           bool writer = true) {
   __shared__ int32_t s_cnt[kGroupWaves][kGroupMaxE];   // per-wave counts, then cursors
   __shared__ int32_t s_base[kGroupMaxE];              // first grouped position of expert e
   __shared__ int32_t s_scan[kGroupThreads];
@@ -265,7 +266,7 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     if (tot > 0) {
       const int ng = groups_of(tot, cap);
       const int g = s_scan2[tid] - ng;
-      for (int j = 0; j < ng && g + j < slots; ++j) {
+      for (int j = 0; writer && j < ng && g + j < slots; ++j) {
         eids[g + j] = tid;
         row_off[g + j] = base + j * cap;
       }
@@ -273,18 +274,18 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     }
   }
   const int active = s_scan2[kGroupThreads - 1];
-  for (int g = active + tid; g < slots; g += kGroupThreads) {
+  for (int g = active + tid; writer && g < slots; g += kGroupThreads) {
     eids[g] = 0;
     row_off[g] = (int32_t)N;
   }
   // rows of out-of-range ids have no grouped position: the positions past
   // the valid rows hold -1 (their gathered rows are zero)
   for (int r = s_scan[kGroupThreads - 1] + tid; r < N; r += kGroupThreads) {
-    order[r] = -1;
+    if (writer) order[r] = -1;
     if (order_lds) order_lds[r] = -1;
   }
   __syncthreads();   // every wave's atomicMax on s_max has landed
-  if (tid == 0) {
+  if (writer && tid == 0) {
     row_off[slots] = (int32_t)N;
     info[0] = active;
     info[1] = s_max;
@@ -296,7 +297,7 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
     const bool valid = i < r1;
     int64_t e = valid ? ids[(int64_t)(i / k) * ids_stride + i % k] : -1;
     const bool ok = valid && e >= 0 && e < E;
-    if (valid && !ok) pos[i] = -1;
+    if (writer && valid && !ok) pos[i] = -1;
     uint64_t pending = __builtin_amdgcn_ballot_w64(ok);
     while (pending) {
       const int leader = __builtin_ctzll(pending);
@@ -306,8 +307,10 @@ __device__ __forceinline__ void group_rows(const int64_t* ids, int64_t ids_strid
       if (ok && e == le) {
         const int rank = __builtin_popcountll(mask & ((1ull << lane) - 1ull));
         const int p = s_base[le] + cur + rank;
-        order[p] = (int32_t)i;
-        pos[i] = p;
+        if (writer) {
+          order[p] = (int32_t)i;
+          pos[i] = p;
+        }
         if (order_lds) order_lds[p] = (int32_t)i;
       }
       if (lane == leader) s_cnt[wave][le] = cur + __builtin_popcountll(mask);
@@ -336,7 +339,7 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
                                                 int32_t* __restrict__ order,
                                                 int32_t* __restrict__ pos,
                                                 int32_t* __restrict__ info, int32_t* order_lds,
-                                                int32_t* s_cnt, int32_t* s_base) {
+                                                int32_t* s_cnt, int32_t* s_base, bool writer) {
   const int lane = threadIdx.x & 63;
   const int N = (int)(T * k);
   for (int e = lane; e < E; e += 64) s_cnt[e] = 0;
@@ -382,7 +385,7 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
       s_base[e] = base;
       const int ng = groups_of(c[j], cap);
       for (int t = 0; t < ng; ++t, ++g) {
-        if (g < slots) {
+        if (writer && g < slots) {
           eids[g] = e;
           row_off[g] = base + t * cap;
         }
@@ -394,14 +397,14 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
   const int max_group = (int)wave_max_u32((uint32_t)mx);
   // positions past the valid rows (out-of-range ids) hold -1
   for (int r = __shfl(tot_x, 63, 64) + lane; r < N; r += 64) {
-    order[r] = -1;
+    if (writer) order[r] = -1;
     if (order_lds) order_lds[r] = -1;
   }
-  for (int gg = active + lane; gg < slots; gg += 64) {
+  for (int gg = active + lane; writer && gg < slots; gg += 64) {
     eids[gg] = 0;
     row_off[gg] = (int32_t)N;
   }
-  if (lane == 0) {
+  if (writer && lane == 0) {
     row_off[slots] = (int32_t)N;
     info[0] = active;
     info[1] = max_group;
@@ -420,11 +423,13 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
     const int ej = __builtin_amdgcn_readlane((int)e, j);
     rank += (j < i && ej == (int)e) ? 1 : 0;
   }
-  if (valid && !ok) pos[i] = -1;
+  if (writer && valid && !ok) pos[i] = -1;
   if (ok) {
     const int p = s_base[e] + rank;
-    order[p] = (int32_t)i;
-    pos[i] = p;
+    if (writer) {
+      order[p] = (int32_t)i;
+      pos[i] = p;
+    }
     if (order_lds) order_lds[p] = (int32_t)i;
   }
 }
@@ -438,6 +443,12 @@ __device__ __forceinline__ void group_rows_wave(const int64_t* ids, int64_t T, i
 // grouping each piece is stored to its token's k grouped positions: no load
 // waits on the grouping. Otherwise the rows are gathered after the grouping,
 // eight 16-byte loads in flight per thread.
+// The rows' stores (T * k rows of K, 512 KiB at 16 tokens x top-8 x 2048)
+// are spread over the grid's workgroups: each repeats the top-k and the
+// grouping in its own LDS (a few microseconds of latency, not of
+// bandwidth), only workgroup 0 writes the ids, weights and tables, and
+// workgroup b stores the rows of its slice of x. One workgroup alone is
+// bound by one CU's store rate (16 tokens: 6.6 us for the stores).
 constexpr int kDecodeMaxRows = kGroupWaves * kRouteMaxK;   // T * k <= 1024
 constexpr int kDecodeHold = 8;
 
@@ -455,17 +466,22 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
   __shared__ int32_t s_cnt1[kGroupMaxE], s_base1[kGroupMaxE];
   __shared__ int32_t s_valid;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
+  const bool writer = wg == 0;
   const int N = (int)(T * k);
   // 32-bit index math (the host checks T * k * K < 2^31)
   const int vec = (int)(K / 8);
   const int xtot = (int)T * vec;
-  const bool hold = xtot <= kDecodeHold * kGroupThreads;   // uniform
+  // this workgroup's slice of x's 16-byte pieces
+  const int per = nwg == 1 ? xtot : (xtot + nwg - 1) / nwg;
+  const int q_lo = wg * per, q_hi = q_lo + per < xtot ? q_lo + per : xtot;
+  const bool hold = per <= kDecodeHold * kGroupThreads;   // uniform
   u32x4_t xv[kDecodeHold];
   if (hold) {
 #pragma unroll
     for (int u = 0; u < kDecodeHold; ++u) {
-      const int q = threadIdx.x + u * kGroupThreads;
-      if (q < xtot) {
+      const int q = q_lo + threadIdx.x + u * kGroupThreads;
+      if (q < q_hi) {
         const int t = q / vec, c = (q - t * vec) * 8;
         xv[u] = *reinterpret_cast<const u32x4_t*>(x + (int64_t)t * ldx + c);
       }
@@ -477,8 +493,10 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
       float w;
       topk_token<kPerLane>(logits + wave * ld, E, k, mode, norm, lane, sel_i, w);
       if (lane < k) {
-        idx[wave * idx_stride + lane] = sel_i;
-        wts[wave * wts_stride + lane] = bf16_rne(w);
+        if (writer) {
+          idx[wave * idx_stride + lane] = sel_i;
+          wts[wave * wts_stride + lane] = bf16_rne(w);
+        }
         s_ids[wave * k + lane] = sel_i;
       }
     }
@@ -490,9 +508,9 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
   if (N <= 64) {
     if (wave == 0)
       group_rows_wave(s_ids, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order,
-                      s_cnt1, s_base1);
+                      s_cnt1, s_base1, writer);
   } else {
-    group_rows(s_ids, k, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order);
+    group_rows(s_ids, k, T, k, E, slots, cap, eids, row_off, order, pos, info, s_order, writer);
   }
   __syncthreads();
   if (hold) {
@@ -511,8 +529,8 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < kDecodeHold; ++u) {
-      const int q = threadIdx.x + u * kGroupThreads;
-      if (q < xtot) {
+      const int q = q_lo + threadIdx.x + u * kGroupThreads;
+      if (q < q_hi) {
         const int t = q / vec, c = (q - t * vec) * 8;
         for (int j = 0; j < k; ++j) {
           const int p = s_pos[t * k + j];
@@ -522,7 +540,8 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
     }
     // positions past the valid rows gather nothing: zeros
     const int v = s_valid;
-    for (int q = v * vec + threadIdx.x; q < N * vec; q += kGroupThreads) {
+    for (int q = v * vec + wg * kGroupThreads + threadIdx.x; q < N * vec;
+         q += nwg * kGroupThreads) {
       const int r = q / vec, c = (q - r * vec) * 8;
       *reinterpret_cast<u32x4_t*>(a_out + (int64_t)r * lda + c) = u32x4_t{0u, 0u, 0u, 0u};
     }
@@ -530,7 +549,8 @@ __global__ void __launch_bounds__(kGroupThreads) k_route_decode(
   }
   const int total = N * vec;
   constexpr int kInFlight = 8;
-  for (int q0 = threadIdx.x; q0 < total; q0 += kInFlight * kGroupThreads) {
+  for (int q0 = wg * kInFlight * kGroupThreads + threadIdx.x; q0 < total;
+       q0 += nwg * kInFlight * kGroupThreads) {
     u32x4_t v[kInFlight];
 #pragma unroll
     for (int u = 0; u < kInFlight; ++u) {
@@ -695,8 +715,12 @@ int gnf4_hip_route_decode(const float* logits, int64_t ld, int64_t T, int64_t E,
     return -1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int per_lane = (int)((E + 63) / 64);
+  // about 32 KiB of grouped rows per workgroup (one at a token), at most 32
+  int64_t nwg = (T * k * K * 2 + 32767) / 32768;
+  nwg = nwg < 1 ? 1 : nwg > 32 ? 32 : nwg;
 #define GNF4_PRO(P)                                                                           \
-  hipLaunchKernelGGL((k_route_decode<P>), dim3(1), dim3(kGroupThreads), 0, s, logits, ld, T,   \
+  hipLaunchKernelGGL((k_route_decode<P>), dim3((unsigned)nwg), dim3(kGroupThreads), 0, s,     \
+                     logits, ld, T,                                                           \
                      (int)E, k, mode, norm, idx, idx_stride, wts, wts_stride,                  \
                      static_cast<const uint16_t*>(x), ldx, K, slots, cap, eids, row_off, order, \
                      pos, info, static_cast<uint16_t*>(a_out), lda)

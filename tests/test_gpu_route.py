@@ -357,13 +357,15 @@ def test_one_launch_prologue_grouping_with_caller_ids(T, k, E):
     assert torch.count_nonzero(a[-1].float()) == 0
 
 
-@pytest.mark.parametrize("T,K", [(16, 4096), (16, 4104), (3, 256)])
+@pytest.mark.parametrize("T,K", [(16, 4096), (16, 4104), (3, 256), (1, 64), (16, 139264)])
 def test_one_launch_prologue_rows_held_or_gathered(T, K):
-    """The prologue's activation rows: x held in registers from the start
-    and stored to each token's grouped positions (T * K / 8 <= 8 pieces per
-    thread: 16 x 4096 is the edge), or gathered after the grouping (16 x
-    4104): both are gather_rows' bits, zero rows past the valid ones
-    included (one id out of range)."""
+    """The prologue's activation rows, spread over up to 32 workgroups (32
+    KiB of grouped rows each): each workgroup's slice of x held in
+    registers from the start and stored to each token's grouped positions
+    (at most 8 pieces per thread), or, for a slice larger than that (16 x
+    139264: 32 workgroups of 8704 pieces), gathered after the grouping. Both
+    are gather_rows' bits, zero rows past the valid ones included (one id
+    out of range), whichever workgroup stores them."""
     r = _route()
     E, k = 128, 8
     g = torch.Generator().manual_seed(T * 7 + K)
